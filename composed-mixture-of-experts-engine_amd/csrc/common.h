@@ -1,0 +1,114 @@
+// Shared device helpers for the gfx950 MoE hot-path kernels.
+//
+// Element types crossing the C ABI are identified by moe_dtype codes
+// (MOE_F32 = 0, MOE_BF16 = 1).  bf16 values are handled as raw 16-bit
+// patterns; conversion to float is exact and conversion from float rounds to
+// nearest-even (the same rounding torch uses for .to(torch.bfloat16)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "../../include/moe_mi355.h"
+
+namespace moe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float load_f(const void* p, int dt, int64_t i) {
+  return dt == MOE_BF16 ? bf2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_f(void* p, int dt, int64_t i, float v) {
+  if (dt == MOE_BF16)
+    static_cast<uint16_t*>(p)[i] = f2bf(v);
+  else
+    static_cast<float*>(p)[i] = v;
+}
+
+// Pack two floats as two bf16 in one dword (low half = a).
+__device__ __forceinline__ uint32_t pack2bf(float a, float b) {
+  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Reductions inside each aligned group of 16 lanes.
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Top-k ordering: larger value first; on an exact tie the lower index wins.
+__device__ __forceinline__ bool better(float v, int e, float bv, int be) {
+  return v > bv || (v == bv && e < be);
+}
+
+inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// ---- error reporting (host side) ----
+void set_error(const char* fmt, ...);
+int fail_arg(const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---- optional per-kernel timing (host side; off unless moe_prof_enable(1)) ----
+// Brackets one launch with two hipEvents recorded on the launch stream.
+struct ProfScope {
+  ProfScope(const char* name, hipStream_t s);
+  ~ProfScope();
+  int slot;
+  hipStream_t stream;
+};
+
+#define MOE_LAUNCH(name, kernel, grid, block, shm, stream, ...)          \
+  do {                                                                  \
+    ::moe::ProfScope _moe_ps(name, stream);                             \
+    hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);  \
+  } while (0)
+
+}  // namespace moe

@@ -1,0 +1,938 @@
+// Fused top-k router, forward and backward, for gfx950.
+//
+// Forward (bf16 tokens x bf16 gate): one wave owns 16 tokens and streams
+// their rows straight from HBM with 16-byte loads, a prefetch ring of U
+// k-chunks deep; the gate matrix is pre-packed once per call into the
+// B-operand layout of v_mfma_f32_16x16x32_bf16, so every lane reads its
+// gate fragment with one 16-byte load from L2.  Logits stay in the MFMA
+// accumulators (fp32); softmax, top-k and renormalisation run on them in
+// registers, one token per 16-lane row, with xor-shuffle reductions inside
+// the row.  Dispatch counts, mean probabilities and the z statistic are
+// reduced per block in LDS and written as per-block partials, which a
+// single-block finalize kernel sums in a fixed order (deterministic, no
+// float atomics).
+//
+// Other dtype combinations (fp32 tokens, fp32 gate) take a generic path:
+// a VALU logits kernel plus a route-from-logits kernel with the same
+// epilogue semantics.
+//
+// Backward: a per-token kernel forms G = dL/dlogits; dx = G wg^T and
+// dwg = x^T G are then computed by one MFMA kernel tiled over
+// (token chunk, 256 hidden columns): the x tile is read once, staged in
+// LDS, used for the dwg partial, and dx is written through an LDS
+// transpose with 16-byte stores.  dwg partials per token chunk are summed
+// in a fixed order by a second kernel.
+#include <cstdarg>
+#include <mutex>
+
+#include "common.h"
+
+namespace moe {
+
+constexpr int kFwdTokPerBlk = 64;  // 4 waves x 16 tokens
+constexpr int kMaxK = 32;
+constexpr int kMaxE = 256;
+
+// ---------------------------------------------------------------------------
+// Gate pack: wg [H, E] bf16 -> wp[c][nt][lane] (16 bytes each) with
+// element j of lane l = wg[c*32 + (l/16)*8 + j][nt*16 + l%16], zero padded.
+// ---------------------------------------------------------------------------
+__global__ void k_pack_gate(const uint16_t* __restrict__ wg, int H, int E, int NT, i16x8* __restrict__ wp) {
+  const int64_t total = (int64_t)((H + 31) / 32) * NT * 64;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(q & 63);
+    const int64_t r = q >> 6;
+    const int nt = (int)(r % NT);
+    const int c = (int)(r / NT);
+    const int e = nt * 16 + (lane & 15);
+    const int k0 = c * 32 + (lane >> 4) * 8;
+    i16x8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = k0 + j;
+      v[j] = (e < E && k < H) ? (short)wg[(int64_t)k * E + e] : (short)0;
+    }
+    wp[q] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward, bf16 x bf16, MFMA.  NT = ceil(E/16) expert tiles, U = prefetch depth.
+// ---------------------------------------------------------------------------
+template <int NT, int U>
+__global__ __launch_bounds__(256) void k_router_fwd_bf16(
+    const uint16_t* __restrict__ x, const i16x8* __restrict__ wp, const float* __restrict__ bias, int N, int H,
+    int E, int K, int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
+    float* __restrict__ lse_out, int* __restrict__ part_cnt, float* __restrict__ part_p, float* __restrict__ part_z) {
+  __shared__ int s_cnt[NT * 16];
+  __shared__ float s_p[4][NT * 16];
+  __shared__ float s_z[4];
+  __shared__ int s_nf[4];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int t0 = blockIdx.x * kFwdTokPerBlk + wv * 16;
+
+  for (int i = threadIdx.x; i < NT * 16; i += blockDim.x) s_cnt[i] = 0;
+
+  int row = t0 + n;
+  if (row > N - 1) row = N - 1;
+  const i16x8* xa = reinterpret_cast<const i16x8*>(x + (int64_t)row * H) + g;
+  const i16x8* wb = wp + lane;
+  const int nc = H >> 5;
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (t0 < N) {
+    i16x8 a[U];
+    i16x8 b[U][NT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (u < nc) {
+        a[u] = __builtin_nontemporal_load(xa + u * 4);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[(u * NT + nt) * 64];
+      }
+    }
+    for (int c0 = 0; c0 < nc; c0 += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u;
+        if (c < nc) {
+          const i16x8 ca = a[u];
+          i16x8 cb[NT];
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) cb[nt] = b[u][nt];
+          const int cn = c + U;
+          if (cn < nc) {
+            a[u] = __builtin_nontemporal_load(xa + cn * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[(cn * NT + nt) * 64];
+          }
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, ca), __builtin_bit_cast(bf16x8, cb[nt]), acc[nt]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds logits[t0 + g*4 + i][nt*16 + n], i = 0..3 ----
+  float pacc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
+  float zacc = 0.f;
+  int nf = 0;
+  __syncthreads();  // s_cnt zeroed
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tt = t0 + g * 4 + i;
+    const bool valid = tt < N;
+    float lg[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int e = nt * 16 + n;
+      float v = acc[nt][i];
+      if (bias != nullptr && e < E) v += bias[e];
+      if (valid && e < E) {
+        logits_out[(int64_t)tt * E + e] = v;
+        if (!isfinite(v)) ++nf;
+      }
+      if (v != v) v = -INFINITY;  // NaN never wins a top-k slot
+      lg[nt] = (e < E) ? v : -INFINITY;
+    }
+    float m = lg[0];
+#pragma unroll
+    for (int nt = 1; nt < NT; ++nt) m = fmaxf(m, lg[nt]);
+    m = row16_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) s += expf(lg[nt] - m);
+    s = row16_sum(s);
+    const float inv = 1.f / s;
+    const float lse = m + logf(s);
+    if (valid) {
+      if (n == 0) lse_out[tt] = lse;
+      zacc += lse * lse;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) pacc[nt] += expf(lg[nt] - m) * inv;
+    }
+
+    // top-k: K rounds of row argmax; round r's winner is kept by lane r % 16.
+    uint32_t sel = 0;
+    int e_slot0 = 0, e_slot1 = 0;
+    float p_slot0 = 0.f, p_slot1 = 0.f;
+    float psum = 0.f;
+    for (int r = 0; r < K; ++r) {
+      float bv = -INFINITY;
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int e = nt * 16 + n;
+        if (e < E && !((sel >> nt) & 1u) && better(lg[nt], e, bv, be)) {
+          bv = lg[nt];
+          be = e;
+        }
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oe = __shfl_xor(be, o);
+        if (better(ov, oe, bv, be)) {
+          bv = ov;
+          be = oe;
+        }
+      }
+      if ((be & 15) == n) sel |= 1u << (be >> 4);
+      const float pv = expf(bv - m) * inv;
+      psum += pv;
+      if (r == n) {
+        e_slot0 = be;
+        p_slot0 = pv;
+      } else if (r == n + 16) {
+        e_slot1 = be;
+        p_slot1 = pv;
+      }
+    }
+    const float rden = 1.f / fmaxf(psum, 1e-30f);
+    if (valid) {
+      if (n < K) {
+        idx_out[(int64_t)tt * K + n] = e_slot0;
+        store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0 * rden);
+        atomicAdd(&s_cnt[e_slot0], 1);
+      }
+      if (n + 16 < K) {
+        idx_out[(int64_t)tt * K + n + 16] = e_slot1;
+        store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1 * rden);
+        atomicAdd(&s_cnt[e_slot1], 1);
+      }
+    }
+  }
+
+  // ---- per-block partials (fixed-order reductions) ----
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float v = pacc[nt];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (g == 0) s_p[wv][nt * 16 + n] = v;
+  }
+  zacc += __shfl_xor(zacc, 16);
+  zacc += __shfl_xor(zacc, 32);
+  nf = wave_sum(nf);
+  if (lane == 0) {
+    s_z[wv] = zacc;
+    s_nf[wv] = nf;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    part_cnt[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+    part_p[(int64_t)blockIdx.x * E + e] = ((s_p[0][e] + s_p[1][e]) + s_p[2][e]) + s_p[3][e];
+  }
+  if (threadIdx.x == 0) {
+    part_z[2 * blockIdx.x] = ((s_z[0] + s_z[1]) + s_z[2]) + s_z[3];
+    part_z[2 * blockIdx.x + 1] = (float)(s_nf[0] + s_nf[1] + s_nf[2] + s_nf[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic forward: logits by VALU (one wave per token), then route_from_logits.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_logits_generic(const void* __restrict__ x, int x_dt,
+                                                        const void* __restrict__ wg, int w_dt,
+                                                        const float* __restrict__ bias, int N, int H, int E,
+                                                        float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int wpb = blockDim.x >> 6;
+  for (int t = blockIdx.x * wpb + (threadIdx.x >> 6); t < N; t += gridDim.x * wpb) {
+    for (int e0 = 0; e0 < E; e0 += 16) {
+      float acc[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+      for (int h = lane; h < H; h += 64) {
+        const float xv = load_f(x, x_dt, (int64_t)t * H + h);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (e0 + j < E) acc[j] = fmaf(xv, load_f(wg, w_dt, (int64_t)h * E + e0 + j), acc[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float v = wave_sum(acc[j]);
+        if (lane == 0 && e0 + j < E) logits[(int64_t)t * E + e0 + j] = v + (bias ? bias[e0 + j] : 0.f);
+      }
+    }
+  }
+}
+
+// One wave per token; lane holds experts lane, lane+64, lane+128, lane+192.
+__global__ __launch_bounds__(256) void k_route_from_logits(const float* __restrict__ logits, int N, int E, int K,
+                                                           int tok_per_blk, int64_t* __restrict__ idx_out,
+                                                           void* __restrict__ w_out, int w_dt,
+                                                           float* __restrict__ lse_out, int* __restrict__ part_cnt,
+                                                           float* __restrict__ part_p, float* __restrict__ part_z) {
+  __shared__ int s_cnt[kMaxE];
+  __shared__ float s_p[4][kMaxE];
+  __shared__ float s_z[4];
+  __shared__ int s_nf[4];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  int nf = 0;
+  for (int i = threadIdx.x; i < kMaxE; i += blockDim.x) s_cnt[i] = 0;
+  __syncthreads();
+  float pacc[4] = {0.f, 0.f, 0.f, 0.f};
+  float zacc = 0.f;
+  const int tbeg = blockIdx.x * tok_per_blk;
+  const int tend = min(N, tbeg + tok_per_blk);
+  for (int t = tbeg + wv; t < tend; t += 4) {
+    float lg[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      float v = (e < E) ? logits[(int64_t)t * E + e] : -INFINITY;
+      if (e < E && !isfinite(v)) ++nf;
+      if (v != v) v = -INFINITY;
+      lg[j] = v;
+    }
+    const float m = wave_max(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += expf(lg[j] - m);
+    s = wave_sum(s);
+    const float inv = 1.f / s;
+    const float lse = m + logf(s);
+    if (lane == 0) lse_out[t] = lse;
+    zacc += lse * lse;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pacc[j] += expf(lg[j] - m) * inv;
+    uint32_t sel = 0;
+    int my_e = 0;
+    float my_p = 0.f;
+    float psum = 0.f;
+    for (int r = 0; r < K; ++r) {
+      float bv = -INFINITY;
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && !((sel >> j) & 1u) && better(lg[j], e, bv, be)) {
+          bv = lg[j];
+          be = e;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oe = __shfl_xor(be, o);
+        if (better(ov, oe, bv, be)) {
+          bv = ov;
+          be = oe;
+        }
+      }
+      if ((be & 63) == lane) sel |= 1u << (be >> 6);
+      const float pv = expf(bv - m) * inv;
+      psum += pv;
+      if (r == lane) {
+        my_e = be;
+        my_p = pv;
+      }
+    }
+    const float rden = 1.f / fmaxf(psum, 1e-30f);
+    if (lane < K) {
+      idx_out[(int64_t)t * K + lane] = my_e;
+      store_f(w_out, w_dt, (int64_t)t * K + lane, my_p * rden);
+      atomicAdd(&s_cnt[my_e], 1);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) s_p[wv][e] = pacc[j];
+  }
+  nf = wave_sum(nf);
+  if (lane == 0) {
+    s_z[wv] = zacc;
+    s_nf[wv] = nf;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    part_cnt[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+    part_p[(int64_t)blockIdx.x * E + e] = ((s_p[0][e] + s_p[1][e]) + s_p[2][e]) + s_p[3][e];
+  }
+  if (threadIdx.x == 0) {
+    part_z[2 * blockIdx.x] = ((s_z[0] + s_z[1]) + s_z[2]) + s_z[3];
+    part_z[2 * blockIdx.x + 1] = (float)(s_nf[0] + s_nf[1] + s_nf[2] + s_nf[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Finalize: fixed-order sums of the per-block partials -> cnt, stats.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__ part_cnt,
+                                                         const float* __restrict__ part_p,
+                                                         const float* __restrict__ part_z, int nblk, int N, int E,
+                                                         int K, int64_t* __restrict__ cnt_out,
+                                                         float* __restrict__ stats) {
+  __shared__ float s_c[kMaxE];
+  __shared__ float s_pe[kMaxE];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int64_t c = 0;
+    float p = 0.f;
+    for (int b = 0; b < nblk; ++b) {
+      c += part_cnt[(int64_t)b * E + e];
+      p += part_p[(int64_t)b * E + e];
+    }
+    cnt_out[e] = c;
+    s_c[e] = (float)c;
+    s_pe[e] = p / (float)N;
+    stats[MOE_STATS_HEAD + e] = p / (float)N;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float z = 0.f, nf = 0.f;
+    for (int b = 0; b < nblk; ++b) {
+      z += part_z[2 * b];
+      nf += part_z[2 * b + 1];
+    }
+    double tot = 0.0, mx = 0.0, aux = 0.0;
+    for (int e = 0; e < E; ++e) {
+      tot += s_c[e];
+      mx = fmax(mx, (double)s_c[e]);
+      aux += ((double)s_c[e] / ((double)N * K)) * (double)s_pe[e];
+    }
+    const double mean = tot / E;
+    double var = 0.0;
+    for (int e = 0; e < E; ++e) var += ((double)s_c[e] - mean) * ((double)s_c[e] - mean);
+    stats[0] = z / (float)N;
+    stats[1] = (float)(aux * E);
+    stats[2] = mean < 1e-9 ? 1.f : (float)(mx / mean);
+    stats[3] = (float)mean;
+    stats[4] = E > 1 ? (float)sqrt(var / (E - 1)) : NAN;
+    stats[5] = (float)tot;
+    stats[6] = nf;
+    stats[7] = 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward 1: G = dL/dlogits, one wave per token.  Writes G (f32) and, when
+// gb != nullptr, G rounded to bf16 in a zero-padded [N, ekp] layout.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict__ logits,
+                                                        const int64_t* __restrict__ idx, const void* __restrict__ gw,
+                                                        int gw_dt, const int64_t* __restrict__ cnt,
+                                                        const float* __restrict__ grad_aux,
+                                                        const float* __restrict__ grad_z, float aux_coef,
+                                                        float z_coef, int N, int E, int K, int round_bf16,
+                                                        float* __restrict__ G, uint16_t* __restrict__ gb, int ekp) {
+  const int lane = threadIdx.x & 63;
+  const int wpb = blockDim.x >> 6;
+  const float ga = grad_aux ? grad_aux[0] : 1.f;
+  const float gz = grad_z ? grad_z[0] : 1.f;
+  const float ca = aux_coef * ga * (float)E / (float)N;
+  const float cz = z_coef * gz * 2.f / (float)N;
+  const float inv_nk = 1.f / ((float)N * (float)K);
+  for (int t = blockIdx.x * wpb + (threadIdx.x >> 6); t < N; t += gridDim.x * wpb) {
+    float lg[4], p[4], f[4], gp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      lg[j] = (e < E) ? logits[(int64_t)t * E + e] : -INFINITY;
+      f[j] = (e < E && ca != 0.f) ? (float)cnt[e] * inv_nk : 0.f;
+      gp[j] = 0.f;
+    }
+    const float m = wave_max(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[j] = expf(lg[j] - m);
+      s += p[j];
+    }
+    s = wave_sum(s);
+    const float inv = 1.f / s;
+    const float lse = m + logf(s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] *= inv;
+    if (gw != nullptr) {
+      // S = max(sum v, 1e-30); gwv = sum gw*v; grad_v = gw/S - gwv/S^2
+      float S = 0.f, gwv = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int e = (int)idx[(int64_t)t * K + k];
+        const float v = expf(logits[(int64_t)t * E + e] - m) * inv;
+        const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
+        S += v;
+        gwv += gk * v;
+      }
+      S = fmaxf(S, 1e-30f);
+      const float iS = 1.f / S;
+      for (int k = 0; k < K; ++k) {
+        const int e = (int)idx[(int64_t)t * K + k];
+        const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
+        const float gv = gk * iS - gwv * iS * iS;
+        if ((e & 63) == lane) gp[e >> 6] += gv;
+      }
+    }
+    float inner = 0.f, pf = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      inner += gp[j] * p[j];
+      pf += p[j] * f[j];
+    }
+    inner = wave_sum(inner);
+    pf = wave_sum(pf);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) {
+        float gl = p[j] * (gp[j] - inner);
+        if (ca != 0.f) gl += ca * p[j] * (f[j] - pf);
+        if (cz != 0.f) gl += cz * lse * p[j];
+        if (round_bf16) gl = bf2f(f2bf(gl));
+        G[(int64_t)t * E + e] = gl;
+        if (gb) gb[(int64_t)t * ekp + e] = f2bf(gl);
+      }
+    }
+    if (gb) {
+      for (int e = E + lane; e < ekp; e += 64) gb[(int64_t)t * ekp + e] = 0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward 2 (bf16 x bf16): dx = G wg^T, dwg partial = x^T G, MFMA.
+// Block = 4 waves = 256 hidden columns; grid = (token chunks, H / 256).
+// EK = ekp / 32 (expert k-chunks for dx), NTE = ceil(E / 16) (expert tiles
+// for dwg).
+// ---------------------------------------------------------------------------
+constexpr int kBwdTS = 32;      // tokens per step
+constexpr int kXPitch = 264;    // bf16 elements per LDS row of the x / dx tiles
+template <int EK, int NTE>
+__global__ __launch_bounds__(256) void k_router_dxdw_bf16(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ wg,
+                                                          const uint16_t* __restrict__ gb, int N, int H, int E,
+                                                          int tc_len, uint16_t* __restrict__ dx,
+                                                          float* __restrict__ ws_dw) {
+  constexpr int EKP = EK * 32;
+  constexpr int GP = EKP + 8;          // row pitch of the token-major G tile
+  constexpr int GTP = kBwdTS + 8;      // row pitch of the expert-major G tile
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kBwdTS * kXPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t dxs[kBwdTS * kXPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t gs[kBwdTS * GP];
+  __shared__ __attribute__((aligned(16))) uint16_t gts[NTE * 16 * GTP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int hb0 = blockIdx.y * 256;
+  const int wcol0 = hb0 + wv * 64;  // this wave's first hidden column
+  const bool wave_active = wcol0 < H;
+  const int tbeg = blockIdx.x * tc_len;
+  const int tend = min(N, tbeg + tc_len);
+
+  for (int i = tid; i < NTE * 16 * GTP; i += 256) gts[i] = 0;
+
+  // gate fragments for dx (B operand: B[k=e][n=h] = wg[h][e]), loaded once.
+  i16x8 wB[4][EK];
+#pragma unroll
+  for (int nc = 0; nc < 4; ++nc) {
+    const int h = wcol0 + nc * 16 + n;
+#pragma unroll
+    for (int ek = 0; ek < EK; ++ek) {
+      i16x8 v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = ek * 32 + g * 8 + j;
+        v[j] = (wave_active && h < H && e < E) ? (short)wg[(int64_t)h * E + e] : (short)0;
+      }
+      wB[nc][ek] = v;
+    }
+  }
+
+  f32x4 accw[4][NTE];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ne = 0; ne < NTE; ++ne) accw[mt][ne] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // x tile load mapping: 32 rows x 256 cols = 1024 chunks of 8 bf16; 4 per thread.
+  u32x4 xr[4];
+  auto load_x = [&](int ts0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int q = tid + 256 * j;
+      const int r = q >> 5;
+      const int col = hb0 + (q & 31) * 8;
+      const int t = ts0 + r;
+      if (t < tend && col < H)
+        xr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + (int64_t)t * H + col));
+      else
+        xr[j] = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  if (tbeg < tend) load_x(tbeg);
+
+  for (int ts0 = tbeg; ts0 < tend; ts0 += kBwdTS) {
+    __syncthreads();  // previous step done with xs / dxs / gs / gts
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int q = tid + 256 * j;
+      const int r = q >> 5;
+      *reinterpret_cast<u32x4*>(&xs[r * kXPitch + (q & 31) * 8]) = xr[j];
+    }
+    // G tile (bf16): token-major gs[t][e] and expert-major gts[e][t]
+    for (int q = tid; q < kBwdTS * EKP; q += 256) {
+      const int r = q / EKP;
+      const int e = q % EKP;
+      const int t = ts0 + r;
+      const uint16_t v = (t < tend) ? gb[(int64_t)t * EKP + e] : (uint16_t)0;
+      gs[r * GP + e] = v;
+      if (e < NTE * 16) gts[e * GTP + r] = v;
+    }
+    if (ts0 + kBwdTS < tend) load_x(ts0 + kBwdTS);
+    __syncthreads();
+
+    if (wave_active) {
+      // ---- dwg partial: D[m=h][n=e] += sum_t x[t][h] G[t][e] ----
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int col = wv * 64 + mt * 16 + n;
+        i16x8 a;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = (short)xs[(g * 8 + j) * kXPitch + col];
+#pragma unroll
+        for (int ne = 0; ne < NTE; ++ne) {
+          const i16x8 b = *reinterpret_cast<const i16x8*>(&gts[(ne * 16 + n) * GTP + g * 8]);
+          accw[mt][ne] =
+              mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), accw[mt][ne]);
+        }
+      }
+      // ---- dx: D[m=t][n=h] = sum_e G[t][e] wg[h][e] ----
+#pragma unroll
+      for (int mk = 0; mk < 2; ++mk) {
+        i16x8 a[EK];
+#pragma unroll
+        for (int ek = 0; ek < EK; ++ek)
+          a[ek] = *reinterpret_cast<const i16x8*>(&gs[(mk * 16 + n) * GP + ek * 32 + g * 8]);
+#pragma unroll
+        for (int nc = 0; nc < 4; ++nc) {
+          f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ek = 0; ek < EK; ++ek)
+            d = mfma16x16x32(__builtin_bit_cast(bf16x8, a[ek]), __builtin_bit_cast(bf16x8, wB[nc][ek]), d);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            dxs[(mk * 16 + g * 4 + i) * kXPitch + wv * 64 + nc * 16 + n] = f2bf(d[i]);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int q = tid + 256 * j;
+      const int r = q >> 5;
+      const int col = hb0 + (q & 31) * 8;
+      const int t = ts0 + r;
+      if (t < tend && col < H)
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&dxs[r * kXPitch + (q & 31) * 8]),
+                                    reinterpret_cast<u32x4*>(dx + (int64_t)t * H + col));
+    }
+  }
+
+  if (wave_active) {
+    float* out = ws_dw + (int64_t)blockIdx.x * H * E;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int ne = 0; ne < NTE; ++ne)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int h = wcol0 + mt * 16 + g * 4 + i;
+          const int e = ne * 16 + n;
+          if (h < H && e < E) out[(int64_t)h * E + e] = accw[mt][ne][i];
+        }
+  }
+}
+
+// Generic dx = G wg^T: one thread per (t, h).
+__global__ __launch_bounds__(256) void k_router_dx_generic(const float* __restrict__ G, const void* __restrict__ wg,
+                                                           int w_dt, int N, int H, int E, void* __restrict__ dx,
+                                                           int x_dt) {
+  const int64_t total = (int64_t)N * H;
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = q / H;
+    const int h = (int)(q % H);
+    float acc = 0.f;
+    for (int e = 0; e < E; ++e) acc = fmaf(G[t * E + e], load_f(wg, w_dt, (int64_t)h * E + e), acc);
+    store_f(dx, x_dt, q, acc);
+  }
+}
+
+// Generic dwg partial per token chunk: thread per (h, e).
+__global__ __launch_bounds__(256) void k_router_dw_generic(const void* __restrict__ x, int x_dt,
+                                                           const float* __restrict__ G, int N, int H, int E,
+                                                           int tc_len, float* __restrict__ ws_dw) {
+  const int64_t he = (int64_t)H * E;
+  const int tbeg = blockIdx.y * tc_len;
+  const int tend = min(N, tbeg + tc_len);
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < he; q += (int64_t)gridDim.x * blockDim.x) {
+    const int h = (int)(q / E);
+    const int e = (int)(q % E);
+    float acc = 0.f;
+    for (int t = tbeg; t < tend; ++t) acc = fmaf(load_f(x, x_dt, (int64_t)t * H + h), G[(int64_t)t * E + e], acc);
+    ws_dw[(int64_t)blockIdx.y * he + q] = acc;
+  }
+}
+
+// dwg = sum over token chunks (fixed order).
+__global__ __launch_bounds__(256) void k_reduce_chunks(const float* __restrict__ ws, int nchunk, int64_t len,
+                                                       void* __restrict__ out, int out_dt) {
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < len; q += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int c = 0; c < nchunk; ++c) acc += ws[(int64_t)c * len + q];
+    store_f(out, out_dt, q, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+struct FwdPlan {
+  bool mfma;
+  int NT;
+  int nblk;
+  size_t off_wp, off_cnt, off_p, off_z, total;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
+  FwdPlan p{};
+  p.mfma = x_dt == MOE_BF16 && w_dt == MOE_BF16 && H % 32 == 0 && E <= 128;
+  p.NT = (int)((E + 15) / 16);
+  if (p.NT == 3) p.NT = 4;
+  if (p.NT > 4 && p.NT < 8) p.NT = 8;
+  if (p.mfma) {
+    p.nblk = cdiv(N, kFwdTokPerBlk);
+  } else {
+    p.nblk = (int)std::min<int64_t>(512, std::max<int64_t>(1, (N + 15) / 16));
+  }
+  size_t off = 0;
+  p.off_wp = off;
+  off += p.mfma ? align256((size_t)((H + 31) / 32) * p.NT * 64 * 16) : 0;
+  p.off_cnt = off;
+  off += align256((size_t)p.nblk * E * sizeof(int));
+  p.off_p = off;
+  off += align256((size_t)p.nblk * E * sizeof(float));
+  p.off_z = off;
+  off += align256((size_t)p.nblk * 2 * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+struct BwdPlan {
+  bool mfma;
+  int EK, NTE;
+  int nchunk, tc_len;
+  size_t off_g, off_gb, off_ws, total;
+};
+
+BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
+  BwdPlan p{};
+  p.mfma = x_dt == MOE_BF16 && w_dt == MOE_BF16 && H % 64 == 0 && E <= 128;
+  p.EK = (int)((E + 31) / 32);
+  if (p.EK == 3) p.EK = 4;
+  p.NTE = (int)((E + 15) / 16);
+  if (p.NTE == 3) p.NTE = 4;
+  if (p.NTE > 4 && p.NTE < 8) p.NTE = 8;
+  if (p.mfma) {
+    const int nhb = cdiv(H, 256);
+    int nchunk = std::max(1, 1024 / nhb);
+    const int max_chunks = cdiv(N, kBwdTS);
+    nchunk = std::min(nchunk, max_chunks);
+    p.tc_len = cdiv(cdiv(N, nchunk), kBwdTS) * kBwdTS;
+    p.nchunk = cdiv(N, p.tc_len);
+  } else {
+    p.tc_len = 256;
+    p.nchunk = cdiv(N, p.tc_len);
+  }
+  if (p.nchunk < 1) p.nchunk = 1;
+  size_t off = 0;
+  p.off_g = off;
+  off += align256((size_t)N * E * sizeof(float));
+  p.off_gb = off;
+  off += p.mfma ? align256((size_t)N * p.EK * 32 * sizeof(uint16_t)) : 0;
+  p.off_ws = off;
+  off += align256((size_t)p.nchunk * H * E * sizeof(float));
+  p.total = off;
+  return p;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int NT>
+void launch_fwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const i16x8* wp, const float* bias, int N, int H,
+                     int E, int K, int64_t* idx, void* w, int w_dt, float* logits, float* lse, int* pc, float* pp,
+                     float* pz) {
+  constexpr int U = NT == 1 ? 16 : (NT == 2 ? 8 : 4);
+  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_bf16<NT, U>), grid, dim3(256), 0, s, x, wp, bias, N, H, E, K, idx, w, w_dt,
+                     logits, lse, pc, pp, pz);
+}
+
+template <int EK, int NTE>
+void launch_dxdw(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* wg, const uint16_t* gb, int N, int H,
+                 int E, int tc_len, uint16_t* dx, float* ws) {
+  MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_bf16<EK, NTE>), grid, dim3(256), 0, s, x, wg, gb, N, H, E, tc_len, dx, ws);
+}
+
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype) {
+  (void)K;
+  if (N <= 0 || H <= 0 || E <= 0) return 0;
+  return plan_fwd(N, H, E, x_dtype, wg_dtype).total;
+}
+
+extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias, int64_t N,
+                              int64_t H, int64_t E, int64_t K, int64_t* idx_out, void* w_out, int w_dtype,
+                              float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out, void* workspace,
+                              size_t ws_bytes, void* stream) {
+  if (N < 0 || H <= 0 || E < 1 || E > kMaxE || K < 1 || K > E || K > kMaxK)
+    return fail_arg("moe_router_fwd: bad shape N=%lld H=%lld E=%lld K=%lld (need 1<=K<=min(E,32), E<=256)",
+                    (long long)N, (long long)H, (long long)E, (long long)K);
+  if (N > INT32_MAX / 2 || H > INT32_MAX / 2) return fail_arg("moe_router_fwd: N or H too large");
+  if ((x_dtype != MOE_F32 && x_dtype != MOE_BF16) || (wg_dtype != MOE_F32 && wg_dtype != MOE_BF16) ||
+      (w_dtype != MOE_F32 && w_dtype != MOE_BF16))
+    return fail_arg("moe_router_fwd: unsupported dtype");
+  if (N == 0) return 0;
+  if (!x || !wg || !idx_out || !w_out || !logits_out || !lse_out || !cnt_out || !stats_out)
+    return fail_arg("moe_router_fwd: null pointer argument");
+  const FwdPlan p = plan_fwd(N, H, E, x_dtype, wg_dtype);
+  if (ws_bytes < p.total || (!workspace && p.total))
+    return set_error("moe_router_fwd: workspace %zu < %zu bytes", ws_bytes, p.total), MOE_EWORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  int* pc = reinterpret_cast<int*>(ws + p.off_cnt);
+  float* pp = reinterpret_cast<float*>(ws + p.off_p);
+  float* pz = reinterpret_cast<float*>(ws + p.off_z);
+  const bool mfma = p.mfma && aligned16(x);
+  if (mfma) {
+    i16x8* wp = reinterpret_cast<i16x8*>(ws + p.off_wp);
+    const int64_t lanes = (int64_t)((H + 31) / 32) * p.NT * 64;
+    MOE_LAUNCH("k_pack_gate", k_pack_gate, dim3((unsigned)std::min<int64_t>(1024, (lanes + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(wg), (int)H, (int)E, p.NT, wp);
+    const dim3 grid(p.nblk);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    switch (p.NT) {
+      case 1: launch_fwd_mfma<1>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
+      case 2: launch_fwd_mfma<2>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
+      case 4: launch_fwd_mfma<4>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
+      case 8: launch_fwd_mfma<8>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
+      default: return fail_arg("moe_router_fwd: internal tile error");
+    }
+    if (int rc = check_launch("k_router_fwd_bf16")) return rc;
+    MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(256), 0, s, pc, pp, pz, p.nblk, (int)N, (int)E, (int)K,
+                       cnt_out, stats_out);
+  } else {
+    FwdPlan pg = p;
+    if (p.mfma) {  // unaligned x: generic path needs its own block count
+      pg = plan_fwd(N, H, E, MOE_F32, MOE_F32);
+      if (ws_bytes < pg.total) return set_error("moe_router_fwd: workspace too small"), MOE_EWORKSPACE;
+      pc = reinterpret_cast<int*>(ws + pg.off_cnt);
+      pp = reinterpret_cast<float*>(ws + pg.off_p);
+      pz = reinterpret_cast<float*>(ws + pg.off_z);
+    }
+    const unsigned lg_blocks = (unsigned)std::min<int64_t>(4096, (N + 3) / 4);
+    MOE_LAUNCH("k_logits_generic", k_logits_generic, dim3(lg_blocks), dim3(256), 0, s, x, x_dtype, wg, wg_dtype, bias, (int)N,
+                       (int)H, (int)E, logits_out);
+    const int tpb = cdiv(N, pg.nblk);
+    const int nblk = cdiv(N, tpb);
+    MOE_LAUNCH("k_route_from_logits", k_route_from_logits, dim3(nblk), dim3(256), 0, s, logits_out, (int)N, (int)E, (int)K, tpb,
+                       idx_out, w_out, w_dtype, lse_out, pc, pp, pz);
+    MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(256), 0, s, pc, pp, pz, nblk, (int)N, (int)E, (int)K,
+                       cnt_out, stats_out);
+  }
+  return check_launch("moe_router_fwd");
+}
+
+extern "C" size_t moe_router_bwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype) {
+  (void)K;
+  if (N <= 0 || H <= 0 || E <= 0) return 0;
+  return plan_bwd(N, H, E, x_dtype, wg_dtype).total;
+}
+
+extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* logits,
+                              const int64_t* idx, const void* grad_w, int gw_dtype, const int64_t* cnt,
+                              const float* grad_aux, const float* grad_z, float aux_coef, float z_coef, int64_t N,
+                              int64_t H, int64_t E, int64_t K, void* dx_out, void* dwg_out, void* workspace,
+                              size_t ws_bytes, void* stream) {
+  if (N < 0 || H <= 0 || E < 1 || E > kMaxE || K < 1 || K > E)
+    return fail_arg("moe_router_bwd: bad shape N=%lld H=%lld E=%lld K=%lld", (long long)N, (long long)H,
+                    (long long)E, (long long)K);
+  if ((x_dtype != MOE_F32 && x_dtype != MOE_BF16) || (wg_dtype != MOE_F32 && wg_dtype != MOE_BF16) ||
+      (gw_dtype != MOE_F32 && gw_dtype != MOE_BF16))
+    return fail_arg("moe_router_bwd: unsupported dtype");
+  if (!x || !wg || !logits || !idx || !dx_out || !dwg_out) return fail_arg("moe_router_bwd: null pointer argument");
+  if (aux_coef != 0.f && !cnt) return fail_arg("moe_router_bwd: aux_coef != 0 needs cnt");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const BwdPlan p = plan_bwd(N > 0 ? N : 1, H, E, x_dtype, wg_dtype);
+  if (N == 0) {
+    const int64_t len = H * E;
+    // dwg = 0 when there are no tokens
+    MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks, dim3((unsigned)std::min<int64_t>(1024, (len + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const float*>(nullptr), 0, len, dwg_out, wg_dtype);
+    return check_launch("moe_router_bwd");
+  }
+  if (ws_bytes < p.total || !workspace)
+    return set_error("moe_router_bwd: workspace %zu < %zu bytes", ws_bytes, p.total), MOE_EWORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  float* G = reinterpret_cast<float*>(ws + p.off_g);
+  float* wsdw = reinterpret_cast<float*>(ws + p.off_ws);
+  const bool mfma = p.mfma && aligned16(x) && aligned16(dx_out);
+  uint16_t* gb = mfma ? reinterpret_cast<uint16_t*>(ws + p.off_gb) : nullptr;
+  const unsigned gl_blocks = (unsigned)std::min<int64_t>(8192, (N + 3) / 4);
+  MOE_LAUNCH("k_router_glogits", k_router_glogits, dim3(gl_blocks), dim3(256), 0, s, logits, idx, grad_w, gw_dtype, cnt, grad_aux,
+                     grad_z, aux_coef, z_coef, (int)N, (int)E, (int)K, (int)(x_dtype == MOE_BF16), G, gb,
+                     p.EK * 32);
+  if (int rc = check_launch("k_router_glogits")) return rc;
+  int nchunk = p.nchunk;
+  if (mfma) {
+    const dim3 grid(p.nchunk, cdiv(H, 256));
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const uint16_t* wb = static_cast<const uint16_t*>(wg);
+    uint16_t* dxb = static_cast<uint16_t*>(dx_out);
+#define MOE_DXDW(EKv, NTEv) \
+  launch_dxdw<EKv, NTEv>(grid, s, xb, wb, gb, (int)N, (int)H, (int)E, p.tc_len, dxb, wsdw)
+    if (p.EK == 1 && p.NTE == 1) MOE_DXDW(1, 1);
+    else if (p.EK == 1 && p.NTE == 2) MOE_DXDW(1, 2);
+    else if (p.EK == 2 && p.NTE == 4) MOE_DXDW(2, 4);
+    else if (p.EK == 4 && p.NTE == 8) MOE_DXDW(4, 8);
+    else return fail_arg("moe_router_bwd: internal tile error");
+#undef MOE_DXDW
+    if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+  } else {
+    const int64_t NH = N * H;
+    MOE_LAUNCH("k_router_dx_generic", k_router_dx_generic, dim3((unsigned)std::min<int64_t>(16384, (NH + 255) / 256)), dim3(256), 0,
+                       s, G, wg, wg_dtype, (int)N, (int)H, (int)E, dx_out, x_dtype);
+    const int64_t he = H * E;
+    // the workspace holds p.nchunk partials of p.tc_len tokens each
+    const dim3 grid((unsigned)std::min<int64_t>(64, (he + 255) / 256), p.nchunk);
+    MOE_LAUNCH("k_router_dw_generic", k_router_dw_generic, grid, dim3(256), 0, s, x, x_dtype, G, (int)N, (int)H, (int)E, p.tc_len,
+                       wsdw);
+    if (int rc = check_launch("k_router_dw_generic")) return rc;
+  }
+  const int64_t len = H * E;
+  MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks, dim3((unsigned)std::min<int64_t>(1024, (len + 255) / 256)), dim3(256), 0, s,
+                     wsdw, nchunk, len, dwg_out, wg_dtype);
+  return check_launch("moe_router_bwd");
+}

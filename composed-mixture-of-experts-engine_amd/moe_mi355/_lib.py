@@ -1,0 +1,146 @@
+"""ctypes binding of libmoe_mi355.so (the C ABI in include/moe_mi355.h).
+
+The library is loaded lazily on first use.  A missing library or a non-ROCm
+device raises immediately: there is no CPU fallback in the product path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmoe_mi355.so")
+
+MOE_F32 = 0
+MOE_BF16 = 1
+STATS_HEAD = 8
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "moe_version": (ctypes.c_char_p, []),
+    "moe_last_error": (_I32, [ctypes.c_char_p, _SZ]),
+    "moe_prof_enable": (_I32, [_I32]),
+    "moe_prof_summary": (_I32, [ctypes.c_char_p, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
+    "moe_prof_kernel_name": (_I32, [_I64, ctypes.c_char_p, _SZ]),
+    "moe_router_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
+    "moe_router_fwd": (
+        _I32,
+        [_P, _I32, _P, _I32, _P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
+    "moe_router_bwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
+    "moe_router_bwd": (
+        _I32,
+        [_P, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _F32, _F32, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def load() -> ctypes.CDLL:
+    """Load libmoe_mi355.so and declare every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                    "(or python moe_mi355/build.py) on a host with ROCm/hipcc"
+                )
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    buf = ctypes.create_string_buffer(512)
+    load().moe_last_error(buf, 512)
+    return buf.value.decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = last_error()
+        if rc < 0:
+            raise ValueError(f"{what}: {msg} (code {rc})")
+        raise RuntimeError(f"{what}: {msg} (hip error {rc})")
+
+
+def prof_enable(on: bool) -> None:
+    """Start (and clear) or stop per-kernel hipEvent timing inside the library."""
+    load().moe_prof_enable(1 if on else 0)
+
+
+def prof_summary() -> dict:
+    """{kernel name: (launches, total ms)} for the launches recorded since prof_enable(True)."""
+    lib = load()
+    out = {}
+    buf = ctypes.create_string_buffer(256)
+    i = 0
+    while lib.moe_prof_kernel_name(i, buf, 256):
+        name = buf.value.decode()
+        n = _I64(0)
+        ms = ctypes.c_double(0.0)
+        check(lib.moe_prof_summary(name.encode(), ctypes.byref(n), ctypes.byref(ms)), "moe_prof_summary")
+        out[name] = (int(n.value), float(ms.value))
+        i += 1
+    return out
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return MOE_F32
+    if dt == torch.bfloat16:
+        return MOE_BF16
+    raise TypeError(f"moe_mi355 supports float32 and bfloat16 tensors, got {dt}")
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must live on one ROCm device; CPU tensors are rejected."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "moe_mi355 runs on an AMD Instinct GPU (gfx950) only; got a tensor on "
+                f"{t.device}. Move the module and inputs to the GPU."
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"moe_mi355: tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

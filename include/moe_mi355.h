@@ -1,0 +1,119 @@
+/*
+ * moe_mi355.h -- C ABI of the MI355X (gfx950) MoE hot-path library
+ * (libmoe_mi355.so).
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless stated otherwise; the
+ *    caller owns all memory, including the workspace (size it with the
+ *    matching *_workspace() query).  The library never allocates device
+ *    memory and keeps no reference to any buffer after the call returns.
+ *  - `stream` is a hipStream_t passed as void*; all work is enqueued on it
+ *    and nothing synchronises the host.
+ *  - Return value: 0 on success, a negative MOE_E* code for a bad argument,
+ *    or a positive hipError_t from a failed launch.  moe_last_error() returns
+ *    the message of the last failure on the calling thread.
+ *  - Element types: MOE_F32 (float32) and MOE_BF16 (bfloat16, raw bits).
+ *    Index tensors are int64 (torch.long) unless named *_i32.
+ *
+ * Reference paths below are relative to moe-engine/ in the reference tree.
+ */
+#ifndef MOE_MI355_H
+#define MOE_MI355_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum moe_dtype { MOE_F32 = 0, MOE_BF16 = 1 };
+
+enum moe_status {
+  MOE_OK = 0,
+  MOE_EINVAL = -1,   /* bad shape / dtype / pointer argument */
+  MOE_EWORKSPACE = -2 /* workspace smaller than the *_workspace() query */
+};
+
+/* Number of float slots in the router `stats` output before the per-expert
+ * mean-probability block.  Layout of stats[MOE_STATS_HEAD + E]:
+ *   [0] z_stat      mean_t (logsumexp_e logits[t,e])^2
+ *   [1] aux_raw     E * sum_e (cnt_e / (N K)) * (mean_t p[t,e])
+ *   [2] imbalance   max(cnt) / mean(cnt), 1.0 if mean(cnt) < 1e-9
+ *   [3] cnt_mean    mean(cnt)
+ *   [4] cnt_std     unbiased standard deviation of cnt
+ *   [5] cnt_total   sum(cnt)  (== N*K when every slot was dispatched)
+ *   [6] nonfinite   number of non-finite logits
+ *   [7] reserved
+ *   [8 + e]         mean_t p[t,e]
+ */
+#define MOE_STATS_HEAD 8
+
+const char* moe_version(void);
+int moe_last_error(char* buf, size_t len);
+
+/* Optional per-kernel timing for benchmarks (no counterpart in the
+ * reference, which times its Triton launch with CUDA events inside the hot
+ * path, pkg/kernels/moe_router.py L:313-343).  Off by default; when on, every
+ * kernel launch is bracketed by two hipEvents recorded on its stream.
+ * moe_prof_enable(1) clears the records and starts recording,
+ * moe_prof_enable(0) stops recording and keeps them.  moe_prof_summary() waits for
+ * the recorded events of `kernel` (NULL = all kernels) and returns the launch
+ * count and total milliseconds.  moe_prof_kernel_name(i, ...) copies the i-th
+ * distinct kernel name seen (launch order) and returns 1, or 0 past the end. */
+int moe_prof_enable(int on);
+int moe_prof_summary(const char* kernel, int64_t* launches, double* total_ms);
+int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
+
+/* ------------------------------------------------------------------------
+ * Router forward: logits = x @ wg (+ bias), p = softmax(logits), top-k of p
+ * (descending, exact ties -> lower expert index), w = v / max(sum v, 1e-30),
+ * dispatch counts and the router statistics above.
+ *
+ * Replaces _triton_forward / _router_fwd_kernel
+ * (pkg/kernels/moe_router.py L:297-388, L:102-176) and the per-forward
+ * bookkeeping of MoERouter.forward: bincount (L:690), z-loss (L:603-612,
+ * L:727-733), load imbalance (L:594-600), count mean/std (L:736-745).
+ *
+ *   x        [N, H]  x_dtype          wg [H, E] wg_dtype      bias [E] f32 or NULL
+ *   idx_out  [N, K]  int64            w_out [N, K] w_dtype
+ *   logits_out [N, E] f32             lse_out [N] f32
+ *   cnt_out  [E] int64                stats_out [MOE_STATS_HEAD + E] f32
+ * Limits: 1 <= K <= min(E, 32), 1 <= E <= 256.
+ * ---------------------------------------------------------------------- */
+size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
+int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias,
+                   int64_t N, int64_t H, int64_t E, int64_t K,
+                   int64_t* idx_out, void* w_out, int w_dtype,
+                   float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out,
+                   void* workspace, size_t ws_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Router backward.  G = dL/dlogits [N, E] from
+ *   (a) the top-k/renormalise term for upstream grad_w (NULL = zero),
+ *   (b) aux_coef * grad_aux * d(aux_raw)/dlogits   (grad_aux NULL = 1.0),
+ *   (c) z_coef   * grad_z   * d(z_stat)/dlogits    (grad_z   NULL = 1.0),
+ * then dx = G @ wg^T (x_dtype) and dwg = x^T @ G (wg_dtype).  With bf16
+ * tokens G is rounded to bf16 before the two products, as the reference does
+ * (grad_logits.to(tokens.dtype)).
+ *
+ * Replaces _router_bwd_kernel and MoERouterFunction.backward
+ * (pkg/kernels/moe_router.py L:178-251, L:504-553; fp64 form L:274-291).
+ * The aux / z terms have no counterpart in the reference (its z-loss is a
+ * detached float, L:603-612): d(aux_raw)/dl[t,j] = (E/N) p[t,j] (f_j - sum_e
+ * p[t,e] f_e) with f = cnt/(N K), d(z_stat)/dl[t,j] = (2/N) lse_t p[t,j].
+ * ---------------------------------------------------------------------- */
+size_t moe_router_bwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
+int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg_dtype,
+                   const float* logits, const int64_t* idx, const void* grad_w, int gw_dtype,
+                   const int64_t* cnt, const float* grad_aux, const float* grad_z,
+                   float aux_coef, float z_coef,
+                   int64_t N, int64_t H, int64_t E, int64_t K,
+                   void* dx_out, void* dwg_out,
+                   void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355_H */

@@ -1,0 +1,180 @@
+"""Parity of the fused HIP router (forward + backward) against the float64 CPU
+oracle on the same seeded inputs.
+
+Bars (written here, per the north star): top-k indices and dispatch counts
+bit-exact wherever the float64 top-k probability margin exceeds 1e-6; logits,
+weights, statistics and gradients within 1e-5 max-norm relative error for
+float32 and 2e-2 for bfloat16.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from gpu_util import MARGIN, TOL, assert_rel, dev, say
+from oracle import router as OR
+
+from moe_mi355 import configs, ops
+from moe_mi355.router import RouterCore
+
+pytestmark = pytest.mark.gpu
+
+# (N, H, E, K, x dtype, gate dtype)
+SHAPES = [
+    (4096, 512, 8, 2, torch.float32, torch.float32),      # C1 (generic kernels)
+    (16384, 4096, 8, 2, torch.bfloat16, torch.bfloat16),  # C2 at full size (MFMA kernels)
+    (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),   # ragged token count
+    (64, 64, 8, 8, torch.bfloat16, torch.bfloat16),       # K == E
+    (37, 128, 32, 1, torch.bfloat16, torch.bfloat16),     # K == 1, N < one block
+    (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # C3 expert count
+    (260, 512, 128, 8, torch.bfloat16, torch.bfloat16),   # C5 expert count
+    (100, 96, 10, 3, torch.bfloat16, torch.bfloat16),     # E not a multiple of 16
+    (128, 256, 40, 18, torch.bfloat16, torch.bfloat16),   # K > 16 on the MFMA path
+    (50, 72, 8, 2, torch.bfloat16, torch.bfloat16),       # H % 32 != 0 -> generic path
+    (333, 256, 24, 20, torch.float32, torch.float32),     # K > 16, generic path
+    (200, 64, 8, 2, torch.bfloat16, torch.float32),       # mixed dtypes -> generic path
+]
+
+
+def _ids(s):
+    N, H, E, K, xd, wd = s
+    return f"N{N}-H{H}-E{E}-K{K}-{str(xd)[6:]}-{str(wd)[6:]}"
+
+
+def _inputs(N, H, E, K, xd, wd, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(N, H, generator=g).to(xd)
+    w = (torch.randn(H, E, generator=g) * 0.02 * math.sqrt(4096.0 / H)).to(wd)
+    gw = torch.randn(N, K, generator=g).to(xd)
+    return x, w, gw
+
+
+def _check_forward(x, w, K, bias=None):
+    d = dev()
+    xd, wd = x.to(d), w.to(d)
+    bd = bias.to(d) if bias is not None else None
+    idx, wt, logits, lse, cnt, stats = ops.router_forward(xd, wd, K, bd)
+    torch.cuda.synchronize()
+    ref = OR.route_fwd(x, w, K, bias=bias)
+    tol = TOL[x.dtype]
+    ok = ref["margin"] > MARGIN
+    idx_c = idx.cpu()
+    assert ok.float().mean() > 0.95, "test inputs have too many near-ties"
+    assert torch.equal(idx_c[ok], ref["idx"][ok]), "top-k indices differ where the margin exceeds 1e-6"
+    assert_rel(logits, ref["logits"], 1e-5, "logits")
+    # weights: compare at the device's routing so a near-tie token compares like with like
+    v = ref["probs"].gather(1, idx_c)
+    w_at = v / v.sum(-1, keepdim=True).clamp_min(1e-30)
+    assert_rel(wt.float(), w_at, tol, "weights")
+    cnt_c = cnt.cpu()
+    assert torch.equal(cnt_c, torch.bincount(idx_c.reshape(-1), minlength=w.shape[1]))
+    if bool(ok.all()):
+        assert torch.equal(cnt_c, OR.dispatch_counts(ref["idx"], w.shape[1]))
+    lse_ref = torch.logsumexp(ref["logits"], -1)
+    assert_rel(lse, lse_ref, 1e-5, "lse")
+    st = stats.cpu().double()
+    N, E = ref["probs"].shape
+    cntd = cnt_c.double()
+    assert st[5].item() == N * K
+    assert st[6].item() == 0.0
+    assert abs(st[0].item() - OR.z_stat(ref["logits"])) <= 1e-5 * max(1.0, OR.z_stat(ref["logits"]))
+    P = ref["probs"].mean(0)
+    assert_rel(st[8 : 8 + E], P, 1e-5, "mean probabilities")
+    aux_ref = float(E * ((cntd / (N * K)) * P).sum())
+    assert abs(st[1].item() - aux_ref) <= 1e-5 * aux_ref
+    assert abs(st[2].item() - OR.load_imbalance(cnt_c)) <= 1e-6 * OR.load_imbalance(cnt_c)
+    assert abs(st[3].item() - float(cntd.mean())) <= 1e-6 * float(cntd.mean())
+    if E > 1:
+        assert abs(st[4].item() - float(cntd.std())) <= 1e-5 * max(1.0, float(cntd.std()))
+    return idx, wt, logits, cnt
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+def test_router_forward_parity(shape):
+    N, H, E, K, xd, wd = shape
+    say(f"[router fwd] {_ids(shape)}")
+    x, w, _ = _inputs(N, H, E, K, xd, wd, seed=N + H + E + K)
+    _check_forward(x, w, K)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=_ids)
+@pytest.mark.parametrize("losses", [False, True], ids=["plain", "aux_z"])
+def test_router_backward_parity(shape, losses):
+    N, H, E, K, xd, wd = shape
+    say(f"[router bwd] {_ids(shape)} losses={losses}")
+    x, w, gw = _inputs(N, H, E, K, xd, wd, seed=7 * N + H + E + K)
+    d = dev()
+    alpha, beta = (0.01, 1e-3) if losses else (0.0, 0.0)
+    xd_, wd_ = x.to(d).requires_grad_(True), w.to(d).requires_grad_(True)
+    idx, wt, aux, z, logits, cnt, stats = RouterCore.apply(xd_, wd_, K, alpha, beta, None)
+    loss = (wt.float() * gw.to(d).float()).sum()
+    if losses:
+        loss = loss + aux + z
+    loss.backward()
+    torch.cuda.synchronize()
+    ref = OR.router_full(x, w, K, grad_w=gw, alpha=alpha, beta=beta, idx_override=idx.cpu())
+    tol = TOL[x.dtype]
+    assert_rel(xd_.grad, ref["dX"], tol, "dX")
+    assert_rel(wd_.grad, ref["dW"], tol if w.dtype == torch.float32 or x.dtype == torch.float32 else tol, "dW")
+    if losses:
+        assert abs(aux.item() - float(ref["aux"])) <= 1e-5 * float(ref["aux"])
+        assert abs(z.item() - float(ref["z"])) <= 1e-5 * float(ref["z"])
+
+
+def test_router_c2_full_size_backward():
+    """C2 exactly as the benchmark draws it (seed 1), forward and backward."""
+    cfg = configs.C2
+    say("[router C2 full]")
+    inp = configs.router_inputs(cfg)
+    x, w, gw = inp["x"], inp["gate_w"], inp["grad_w"]
+    idx, _, _, _ = _check_forward(x, w, cfg.K)
+    d = dev()
+    xd_, wd_ = x.to(d).requires_grad_(True), w.to(d).requires_grad_(True)
+    out = RouterCore.apply(xd_, wd_, cfg.K, 0.0, 0.0, None)
+    (out[1].float() * gw.to(d).float()).sum().backward()
+    ref = OR.router_full(x, w, cfg.K, grad_w=gw, idx_override=out[0].cpu())
+    assert_rel(xd_.grad, ref["dX"], 2e-2, "dX")
+    assert_rel(wd_.grad, ref["dW"], 2e-2, "dW")
+
+
+def test_router_deterministic():
+    say("[router determinism]")
+    x, w, gw = _inputs(4096, 1024, 64, 6, torch.bfloat16, torch.bfloat16, seed=5)
+    d = dev()
+    outs = []
+    for _ in range(2):
+        xd_, wd_ = x.to(d).requires_grad_(True), w.to(d).requires_grad_(True)
+        idx, wt, aux, z, logits, cnt, stats = RouterCore.apply(xd_, wd_, 6, 0.01, 1e-3, None)
+        ((wt.float() * gw.to(d).float()).sum() + aux + z).backward()
+        outs.append([t.detach().cpu() for t in (idx, wt, logits, cnt, stats, xd_.grad, wd_.grad)])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_router_exact_ties_take_lowest_index():
+    say("[router ties]")
+    d = dev()
+    N, H, E, K = 100, 64, 8, 3
+    x = torch.randn(N, H).to(torch.bfloat16).to(d)
+    w = torch.zeros(H, E, dtype=torch.bfloat16, device=d)
+    idx, wt, *_ = ops.router_forward(x, w, K)
+    assert torch.equal(idx.cpu(), torch.arange(K).expand(N, K))
+    assert torch.allclose(wt.float().cpu(), torch.full((N, K), 1.0 / K), atol=1e-3)
+
+
+def test_router_with_bias_matches_oracle():
+    say("[router bias]")
+    x, w, _ = _inputs(512, 256, 32, 4, torch.bfloat16, torch.bfloat16, seed=11)
+    bias = configs.zipf_bias(32, torch.Generator().manual_seed(4))
+    _check_forward(x, w, 4, bias=bias)
+
+
+def test_router_empty_batch():
+    d = dev()
+    x = torch.zeros(0, 64, dtype=torch.bfloat16, device=d)
+    w = torch.randn(64, 8, device=d).to(torch.bfloat16)
+    idx, wt, logits, lse, cnt, stats = ops.router_forward(x, w, 2)
+    assert idx.shape == (0, 2) and int(cnt.sum()) == 0
