@@ -29,7 +29,6 @@
 
 namespace moe {
 
-constexpr int kFwdTokPerBlk = 64;  // 4 waves x 16 tokens
 constexpr int kMaxK = 32;
 constexpr int kMaxE = 256;
 
@@ -47,33 +46,44 @@ __global__ void k_pack_gate(const uint16_t* __restrict__ wg, int H, int E, int N
     const int e = nt * 16 + (lane & 15);
     const int k0 = c * 32 + (lane >> 4) * 8;
     i16x8 v;
+    const int ee = min(e, E - 1);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int k = k0 + j;
-      v[j] = (e < E && k < H) ? (short)wg[(int64_t)k * E + e] : (short)0;
+      const short val = (short)wg[(int64_t)min(k, H - 1) * E + ee];  // clamped: always in bounds
+      v[j] = (e < E && k < H) ? val : (short)0;
     }
     wp[q] = v;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Forward, bf16 x bf16, MFMA.  NT = ceil(E/16) expert tiles, U = prefetch depth.
+// Forward, bf16 x bf16, MFMA.
+//   NT: 16-expert tiles (ceil(E/16)).  HS: waves sharing one 16-token group,
+//   each streaming 1/HS of the hidden dim (partial logits are summed in LDS
+//   in a fixed order).  U: 32-wide k-chunks per prefetch group; the main
+//   loop is branch-free and double-buffered (2U chunks in flight per wave).
+// Block = 4 waves = 4/HS token groups of 16 tokens.
 // ---------------------------------------------------------------------------
-template <int NT, int U>
+template <int NT, int HS, int U>
 __global__ __launch_bounds__(256) void k_router_fwd_bf16(
     const uint16_t* __restrict__ x, const i16x8* __restrict__ wp, const float* __restrict__ bias, int N, int H,
     int E, int K, int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
     float* __restrict__ lse_out, int* __restrict__ part_cnt, float* __restrict__ part_p, float* __restrict__ part_z) {
+  constexpr int TG = 4 / HS;
   __shared__ int s_cnt[NT * 16];
-  __shared__ float s_p[4][NT * 16];
-  __shared__ float s_z[4];
-  __shared__ int s_nf[4];
+  __shared__ float s_p[TG][NT * 16];
+  __shared__ float s_z[TG];
+  __shared__ int s_nf[TG];
+  __shared__ f32x4 s_acc[HS > 1 ? (HS - 1) * TG * NT * 64 : 1];
 
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
+  const int tg = wv / HS;
+  const int hp = wv % HS;
   const int g = lane >> 4;
   const int n = lane & 15;
-  const int t0 = blockIdx.x * kFwdTokPerBlk + wv * 16;
+  const int t0 = blockIdx.x * (16 * TG) + tg * 16;
 
   for (int i = threadIdx.x; i < NT * 16; i += blockDim.x) s_cnt[i] = 0;
 
@@ -82,161 +92,198 @@ __global__ __launch_bounds__(256) void k_router_fwd_bf16(
   const i16x8* xa = reinterpret_cast<const i16x8*>(x + (int64_t)row * H) + g;
   const i16x8* wb = wp + lane;
   const int nc = H >> 5;
+  const int per = nc / HS;
+  const int c_beg = hp * per;
+  const int c_end = (hp == HS - 1) ? nc : c_beg + per;
 
   f32x4 acc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (t0 < N) {
-    i16x8 a[U];
-    i16x8 b[U][NT];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (u < nc) {
-        a[u] = __builtin_nontemporal_load(xa + u * 4);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[(u * NT + nt) * 64];
-      }
-    }
-    for (int c0 = 0; c0 < nc; c0 += U) {
+    i16x8 a0[U], a1[U];
+    i16x8 b0[U][NT], b1[U][NT];
+    auto load_grp = [&](i16x8(&a)[U], i16x8(&b)[U][NT], int c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int c = c0 + u;
-        if (c < nc) {
-          const i16x8 ca = a[u];
-          i16x8 cb[NT];
+        a[u] = __builtin_nontemporal_load(xa + (c + u) * 4);
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) cb[nt] = b[u][nt];
-          const int cn = c + U;
-          if (cn < nc) {
-            a[u] = __builtin_nontemporal_load(xa + cn * 4);
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[(cn * NT + nt) * 64];
-          }
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt)
-            acc[nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, ca), __builtin_bit_cast(bf16x8, cb[nt]), acc[nt]);
-        }
+        for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[((c + u) * NT + nt) * 64];
       }
+    };
+    auto mma_grp = [&](const i16x8(&a)[U], const i16x8(&b)[U][NT]) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a[u]), __builtin_bit_cast(bf16x8, b[u][nt]), acc[nt]);
+    };
+    int c = c_beg;
+    const int npair = (c_end - c_beg) / (2 * U);
+    if (npair > 0) {
+      load_grp(a0, b0, c);
+      for (int i = 0; i < npair - 1; ++i) {
+        load_grp(a1, b1, c + U);
+        mma_grp(a0, b0);
+        load_grp(a0, b0, c + 2 * U);
+        mma_grp(a1, b1);
+        c += 2 * U;
+      }
+      load_grp(a1, b1, c + U);
+      mma_grp(a0, b0);
+      mma_grp(a1, b1);
+      c += 2 * U;
+    }
+    for (; c < c_end; ++c) {
+      const i16x8 a = __builtin_nontemporal_load(xa + c * 4);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, wb[(c * NT + nt) * 64]),
+                               acc[nt]);
     }
   }
 
-  // ---- epilogue: lane holds logits[t0 + g*4 + i][nt*16 + n], i = 0..3 ----
-  float pacc[NT];
+  if constexpr (HS > 1) {
+    if (hp > 0) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
-  float zacc = 0.f;
-  int nf = 0;
-  __syncthreads();  // s_cnt zeroed
-
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tt = t0 + g * 4 + i;
-    const bool valid = tt < N;
-    float lg[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int e = nt * 16 + n;
-      float v = acc[nt][i];
-      if (bias != nullptr && e < E) v += bias[e];
-      if (valid && e < E) {
-        logits_out[(int64_t)tt * E + e] = v;
-        if (!isfinite(v)) ++nf;
-      }
-      if (v != v) v = -INFINITY;  // NaN never wins a top-k slot
-      lg[nt] = (e < E) ? v : -INFINITY;
+      for (int nt = 0; nt < NT; ++nt) s_acc[(((hp - 1) * TG + tg) * NT + nt) * 64 + lane] = acc[nt];
     }
-    float m = lg[0];
+  }
+  __syncthreads();  // s_cnt zeroed, partial accumulators visible
+  if constexpr (HS > 1) {
+    if (hp == 0) {
 #pragma unroll
-    for (int nt = 1; nt < NT; ++nt) m = fmaxf(m, lg[nt]);
-    m = row16_max(m);
-    float s = 0.f;
+      for (int q = 1; q < HS; ++q)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) s += expf(lg[nt] - m);
-    s = row16_sum(s);
-    const float inv = 1.f / s;
-    const float lse = m + logf(s);
-    if (valid) {
-      if (n == 0) lse_out[tt] = lse;
-      zacc += lse * lse;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) pacc[nt] += expf(lg[nt] - m) * inv;
+        for (int nt = 0; nt < NT; ++nt) acc[nt] += s_acc[(((q - 1) * TG + tg) * NT + nt) * 64 + lane];
     }
+  }
 
-    // top-k: K rounds of row argmax; round r's winner is kept by lane r % 16.
-    uint32_t sel = 0;
-    int e_slot0 = 0, e_slot1 = 0;
-    float p_slot0 = 0.f, p_slot1 = 0.f;
-    float psum = 0.f;
-    for (int r = 0; r < K; ++r) {
-      float bv = -INFINITY;
-      int be = 0x7fffffff;
+  if (hp == 0) {
+    // ---- epilogue: lane holds logits[t0 + g*4 + i][nt*16 + n], i = 0..3 ----
+    float pacc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
+    float zacc = 0.f;
+    int nf = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tt = t0 + g * 4 + i;
+      const bool valid = tt < N;
+      float lg[NT];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int e = nt * 16 + n;
-        if (e < E && !((sel >> nt) & 1u) && better(lg[nt], e, bv, be)) {
-          bv = lg[nt];
-          be = e;
+        float v = acc[nt][i];
+        if (bias != nullptr && e < E) v += bias[e];
+        if (valid && e < E) {
+          logits_out[(int64_t)tt * E + e] = v;
+          if (!isfinite(v)) ++nf;
         }
+        if (v != v) v = -INFINITY;  // NaN never wins a top-k slot
+        lg[nt] = (e < E) ? v : -INFINITY;
       }
+      float m = lg[0];
 #pragma unroll
-      for (int o = 8; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oe = __shfl_xor(be, o);
-        if (better(ov, oe, bv, be)) {
-          bv = ov;
-          be = oe;
-        }
+      for (int nt = 1; nt < NT; ++nt) m = fmaxf(m, lg[nt]);
+      m = row16_max(m);
+      float s = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) s += expf(lg[nt] - m);
+      s = row16_sum(s);
+      const float inv = 1.f / s;
+      const float lse = m + logf(s);
+      if (valid) {
+        if (n == 0) lse_out[tt] = lse;
+        zacc += lse * lse;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) pacc[nt] += expf(lg[nt] - m) * inv;
       }
-      if ((be & 15) == n) sel |= 1u << (be >> 4);
-      const float pv = expf(bv - m) * inv;
-      psum += pv;
-      if (r == n) {
-        e_slot0 = be;
-        p_slot0 = pv;
-      } else if (r == n + 16) {
-        e_slot1 = be;
-        p_slot1 = pv;
-      }
-    }
-    const float rden = 1.f / fmaxf(psum, 1e-30f);
-    if (valid) {
-      if (n < K) {
-        idx_out[(int64_t)tt * K + n] = e_slot0;
-        store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0 * rden);
-        atomicAdd(&s_cnt[e_slot0], 1);
-      }
-      if (n + 16 < K) {
-        idx_out[(int64_t)tt * K + n + 16] = e_slot1;
-        store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1 * rden);
-        atomicAdd(&s_cnt[e_slot1], 1);
-      }
-    }
-  }
 
-  // ---- per-block partials (fixed-order reductions) ----
+      // top-k: K rounds of row argmax; round r's winner is kept by lane r % 16.
+      uint32_t sel = 0;
+      int e_slot0 = 0, e_slot1 = 0;
+      float p_slot0 = 0.f, p_slot1 = 0.f;
+      float psum = 0.f;
+      for (int r = 0; r < K; ++r) {
+        float bv = -INFINITY;
+        int be = 0x7fffffff;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    float v = pacc[nt];
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    if (g == 0) s_p[wv][nt * 16 + n] = v;
-  }
-  zacc += __shfl_xor(zacc, 16);
-  zacc += __shfl_xor(zacc, 32);
-  nf = wave_sum(nf);
-  if (lane == 0) {
-    s_z[wv] = zacc;
-    s_nf[wv] = nf;
+        for (int nt = 0; nt < NT; ++nt) {
+          const int e = nt * 16 + n;
+          if (e < E && !((sel >> nt) & 1u) && better(lg[nt], e, bv, be)) {
+            bv = lg[nt];
+            be = e;
+          }
+        }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+          const float ov = __shfl_xor(bv, o);
+          const int oe = __shfl_xor(be, o);
+          if (better(ov, oe, bv, be)) {
+            bv = ov;
+            be = oe;
+          }
+        }
+        if ((be & 15) == n) sel |= 1u << (be >> 4);
+        const float pv = expf(bv - m) * inv;
+        psum += pv;
+        if (r == n) {
+          e_slot0 = be;
+          p_slot0 = pv;
+        } else if (r == n + 16) {
+          e_slot1 = be;
+          p_slot1 = pv;
+        }
+      }
+      const float rden = 1.f / fmaxf(psum, 1e-30f);
+      if (valid) {
+        if (n < K) {
+          idx_out[(int64_t)tt * K + n] = e_slot0;
+          store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0 * rden);
+          atomicAdd(&s_cnt[e_slot0], 1);
+        }
+        if (n + 16 < K) {
+          idx_out[(int64_t)tt * K + n + 16] = e_slot1;
+          store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1 * rden);
+          atomicAdd(&s_cnt[e_slot1], 1);
+        }
+      }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float v = pacc[nt];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (g == 0) s_p[tg][nt * 16 + n] = v;
+    }
+    zacc += __shfl_xor(zacc, 16);
+    zacc += __shfl_xor(zacc, 32);
+    nf = wave_sum(nf);
+    if (lane == 0) {
+      s_z[tg] = zacc;
+      s_nf[tg] = nf;
+    }
   }
   __syncthreads();
+  // ---- per-block partials (fixed-order sums over token groups) ----
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float p = 0.f;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) p += s_p[q][e];
     part_cnt[(int64_t)blockIdx.x * E + e] = s_cnt[e];
-    part_p[(int64_t)blockIdx.x * E + e] = ((s_p[0][e] + s_p[1][e]) + s_p[2][e]) + s_p[3][e];
+    part_p[(int64_t)blockIdx.x * E + e] = p;
   }
   if (threadIdx.x == 0) {
-    part_z[2 * blockIdx.x] = ((s_z[0] + s_z[1]) + s_z[2]) + s_z[3];
-    part_z[2 * blockIdx.x + 1] = (float)(s_nf[0] + s_nf[1] + s_nf[2] + s_nf[3]);
+    float z = 0.f;
+    int nfs = 0;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+      z += s_z[q];
+      nfs += s_nf[q];
+    }
+    part_z[2 * blockIdx.x] = z;
+    part_z[2 * blockIdx.x + 1] = (float)nfs;
   }
 }
 
@@ -375,29 +422,87 @@ __global__ __launch_bounds__(256) void k_route_from_logits(const float* __restri
 __global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__ part_cnt,
                                                          const float* __restrict__ part_p,
                                                          const float* __restrict__ part_z, int nblk, int N, int E,
-                                                         int K, int64_t* __restrict__ cnt_out,
-                                                         float* __restrict__ stats) {
+                                                         int K, float aux_coef, float z_coef,
+                                                         int64_t* __restrict__ cnt_out, float* __restrict__ stats,
+                                                         float* __restrict__ aux_out, float* __restrict__ z_out) {
   __shared__ float s_c[kMaxE];
   __shared__ float s_pe[kMaxE];
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int64_t c = 0;
+  __shared__ float s_red[2][4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // threads per expert: a power of two <= 64 so each expert's threads sit in one wave
+  int tpe = 1;
+  while (tpe * 2 <= 64 && tpe * 2 * E <= 256) tpe *= 2;
+  const int epp = 256 / tpe;  // experts per pass
+  for (int e0 = 0; e0 < E; e0 += epp) {
+    const int e = e0 + tid / tpe;
+    const int j = tid % tpe;
+    int c = 0;
     float p = 0.f;
-    for (int b = 0; b < nblk; ++b) {
-      c += part_cnt[(int64_t)b * E + e];
-      p += part_p[(int64_t)b * E + e];
+    if (e < E) {
+      int b = j;
+      for (; b + 7 * tpe < nblk; b += 8 * tpe) {  // 8 independent loads in flight
+        int cv[8];
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          cv[u] = part_cnt[(int64_t)(b + u * tpe) * E + e];
+          pv[u] = part_p[(int64_t)(b + u * tpe) * E + e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          c += cv[u];
+          p += pv[u];
+        }
+      }
+      for (; b < nblk; b += tpe) {
+        c += part_cnt[(int64_t)b * E + e];
+        p += part_p[(int64_t)b * E + e];
+      }
     }
-    cnt_out[e] = c;
-    s_c[e] = (float)c;
-    s_pe[e] = p / (float)N;
-    stats[MOE_STATS_HEAD + e] = p / (float)N;
+    for (int o = tpe / 2; o > 0; o >>= 1) {
+      c += __shfl_xor(c, o);
+      p += __shfl_xor(p, o);
+    }
+    if (j == 0 && e < E) {
+      cnt_out[e] = c;
+      s_c[e] = (float)c;
+      s_pe[e] = p / (float)N;
+      stats[MOE_STATS_HEAD + e] = p / (float)N;
+    }
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float z = 0.f, nf = 0.f;
-    for (int b = 0; b < nblk; ++b) {
+  float z = 0.f, nf = 0.f;
+  {
+    int b = tid;
+    for (; b + 3 * 256 < nblk; b += 4 * 256) {
+      f32x4 zz;
+      float nn[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        zz[u] = part_z[2 * (b + u * 256)];
+        nn[u] = part_z[2 * (b + u * 256) + 1];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        z += zz[u];
+        nf += nn[u];
+      }
+    }
+    for (; b < nblk; b += 256) {
       z += part_z[2 * b];
       nf += part_z[2 * b + 1];
     }
+  }
+  z = wave_sum(z);
+  nf = wave_sum(nf);
+  if (lane == 0) {
+    s_red[0][tid >> 6] = z;
+    s_red[1][tid >> 6] = nf;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    z = ((s_red[0][0] + s_red[0][1]) + s_red[0][2]) + s_red[0][3];
+    nf = ((s_red[1][0] + s_red[1][1]) + s_red[1][2]) + s_red[1][3];
     double tot = 0.0, mx = 0.0, aux = 0.0;
     for (int e = 0; e < E; ++e) {
       tot += s_c[e];
@@ -407,21 +512,27 @@ __global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__
     const double mean = tot / E;
     double var = 0.0;
     for (int e = 0; e < E; ++e) var += ((double)s_c[e] - mean) * ((double)s_c[e] - mean);
-    stats[0] = z / (float)N;
-    stats[1] = (float)(aux * E);
+    const float zstat = z / (float)N;
+    const float aux_raw = (float)(aux * E);
+    stats[0] = zstat;
+    stats[1] = aux_raw;
     stats[2] = mean < 1e-9 ? 1.f : (float)(mx / mean);
     stats[3] = (float)mean;
     stats[4] = E > 1 ? (float)sqrt(var / (E - 1)) : NAN;
     stats[5] = (float)tot;
     stats[6] = nf;
     stats[7] = 0.f;
+    if (aux_out) aux_out[0] = aux_coef * aux_raw;
+    if (z_out) z_out[0] = z_coef * zstat;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward 1: G = dL/dlogits, one wave per token.  Writes G (f32) and, when
-// gb != nullptr, G rounded to bf16 in a zero-padded [N, ekp] layout.
+// Backward 1: G = dL/dlogits.  LPT lanes per token (EPL experts per lane).
+// Writes G (f32) and, when gb != nullptr, G rounded to bf16 in a zero-padded
+// [N, ekp] layout.
 // ---------------------------------------------------------------------------
+template <int LPT, int EPL>
 __global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict__ logits,
                                                         const int64_t* __restrict__ idx, const void* __restrict__ gw,
                                                         int gw_dt, const int64_t* __restrict__ cnt,
@@ -429,34 +540,46 @@ __global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict_
                                                         const float* __restrict__ grad_z, float aux_coef,
                                                         float z_coef, int N, int E, int K, int round_bf16,
                                                         float* __restrict__ G, uint16_t* __restrict__ gb, int ekp) {
+  constexpr int TPW = 64 / LPT;  // tokens per wave
   const int lane = threadIdx.x & 63;
+  const int sub = lane % LPT;
+  const int slot = lane / LPT;
   const int wpb = blockDim.x >> 6;
   const float ga = grad_aux ? grad_aux[0] : 1.f;
   const float gz = grad_z ? grad_z[0] : 1.f;
   const float ca = aux_coef * ga * (float)E / (float)N;
   const float cz = z_coef * gz * 2.f / (float)N;
   const float inv_nk = 1.f / ((float)N * (float)K);
-  for (int t = blockIdx.x * wpb + (threadIdx.x >> 6); t < N; t += gridDim.x * wpb) {
-    float lg[4], p[4], f[4], gp[4];
+  const int stride = gridDim.x * wpb * TPW;
+  for (int tb = (blockIdx.x * wpb + (threadIdx.x >> 6)) * TPW; tb < N; tb += stride) {
+    const int t_raw = tb + slot;
+    const bool valid = t_raw < N;
+    const int t = valid ? t_raw : N - 1;
+    float lg[EPL], p[EPL], f[EPL], gp[EPL];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = lane + 64 * j;
+    for (int j = 0; j < EPL; ++j) {
+      const int e = sub + LPT * j;
       lg[j] = (e < E) ? logits[(int64_t)t * E + e] : -INFINITY;
       f[j] = (e < E && ca != 0.f) ? (float)cnt[e] * inv_nk : 0.f;
       gp[j] = 0.f;
     }
-    const float m = wave_max(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
+    float m = lg[0];
+#pragma unroll
+    for (int j = 1; j < EPL; ++j) m = fmaxf(m, lg[j]);
+#pragma unroll
+    for (int o = LPT / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < EPL; ++j) {
       p[j] = expf(lg[j] - m);
       s += p[j];
     }
-    s = wave_sum(s);
+#pragma unroll
+    for (int o = LPT / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
     const float inv = 1.f / s;
     const float lse = m + logf(s);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p[j] *= inv;
+    for (int j = 0; j < EPL; ++j) p[j] *= inv;
     if (gw != nullptr) {
       // S = max(sum v, 1e-30); gwv = sum gw*v; grad_v = gw/S - gwv/S^2
       float S = 0.f, gwv = 0.f;
@@ -473,31 +596,38 @@ __global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict_
         const int e = (int)idx[(int64_t)t * K + k];
         const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
         const float gv = gk * iS - gwv * iS * iS;
-        if ((e & 63) == lane) gp[e >> 6] += gv;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j)
+          if (e == sub + LPT * j) gp[j] += gv;
       }
     }
     float inner = 0.f, pf = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < EPL; ++j) {
       inner += gp[j] * p[j];
       pf += p[j] * f[j];
     }
-    inner = wave_sum(inner);
-    pf = wave_sum(pf);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E) {
-        float gl = p[j] * (gp[j] - inner);
-        if (ca != 0.f) gl += ca * p[j] * (f[j] - pf);
-        if (cz != 0.f) gl += cz * lse * p[j];
-        if (round_bf16) gl = bf2f(f2bf(gl));
-        G[(int64_t)t * E + e] = gl;
-        if (gb) gb[(int64_t)t * ekp + e] = f2bf(gl);
-      }
+    for (int o = LPT / 2; o > 0; o >>= 1) {
+      inner += __shfl_xor(inner, o);
+      pf += __shfl_xor(pf, o);
     }
-    if (gb) {
-      for (int e = E + lane; e < ekp; e += 64) gb[(int64_t)t * ekp + e] = 0;
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        const int e = sub + LPT * j;
+        if (e < E) {
+          float gl = p[j] * (gp[j] - inner);
+          if (ca != 0.f) gl += ca * p[j] * (f[j] - pf);
+          if (cz != 0.f) gl += cz * lse * p[j];
+          if (round_bf16) gl = bf2f(f2bf(gl));
+          G[(int64_t)t * E + e] = gl;
+          if (gb) gb[(int64_t)t * ekp + e] = f2bf(gl);
+        }
+      }
+      if (gb) {
+        for (int e = E + sub; e < ekp; e += LPT) gb[(int64_t)t * ekp + e] = 0;
+      }
     }
   }
 }
@@ -689,13 +819,43 @@ __global__ __launch_bounds__(256) void k_router_dw_generic(const void* __restric
   }
 }
 
-// dwg = sum over token chunks (fixed order).
+// out = sum over token chunks of ws[c][*], fixed order.  A block covers 64
+// groups of VEC consecutive outputs; its 4 waves sum interleaved chunk
+// subsets, then wave 0 adds the 4 partials in order.
+template <int VEC>
 __global__ __launch_bounds__(256) void k_reduce_chunks(const float* __restrict__ ws, int nchunk, int64_t len,
                                                        void* __restrict__ out, int out_dt) {
-  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < len; q += (int64_t)gridDim.x * blockDim.x) {
-    float acc = 0.f;
-    for (int c = 0; c < nchunk; ++c) acc += ws[(int64_t)c * len + q];
-    store_f(out, out_dt, q, acc);
+  __shared__ float s[4][64][VEC];
+  const int qi = threadIdx.x & 63;
+  const int cg = threadIdx.x >> 6;
+  const int64_t ngroups = len / VEC;
+  for (int64_t gb = (int64_t)blockIdx.x * 64; gb < ngroups; gb += (int64_t)gridDim.x * 64) {
+    const int64_t q = gb + qi;
+    float a[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) a[v] = 0.f;
+    if (q < ngroups && ws != nullptr) {
+      for (int c = cg; c < nchunk; c += 4) {
+        const float* src = ws + (int64_t)c * len + q * VEC;
+        if constexpr (VEC == 4) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) a[v] += x[v];
+        } else {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) a[v] += src[v];
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) s[cg][qi][v] = a[v];
+    __syncthreads();
+    if (cg == 0 && q < ngroups) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v)
+        store_f(out, out_dt, q * VEC + v, ((s[0][qi][v] + s[1][qi][v]) + s[2][qi][v]) + s[3][qi][v]);
+    }
+    __syncthreads();
   }
 }
 
@@ -703,6 +863,11 @@ __global__ __launch_bounds__(256) void k_reduce_chunks(const float* __restrict__
 // Host side
 // ---------------------------------------------------------------------------
 namespace {
+
+// Hidden-dim split (HS) and prefetch depth (U) of the forward kernel per expert-tile count.
+constexpr int fwd_hs(int NT) { return NT == 1 ? 4 : (NT == 2 ? 2 : 1); }
+constexpr int fwd_u(int NT) { return NT <= 4 ? 4 : 2; }
+int fwd_tokens_per_block(int NT) { return 16 * (4 / fwd_hs(NT)); }
 
 struct FwdPlan {
   bool mfma;
@@ -720,7 +885,7 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   if (p.NT == 3) p.NT = 4;
   if (p.NT > 4 && p.NT < 8) p.NT = 8;
   if (p.mfma) {
-    p.nblk = cdiv(N, kFwdTokPerBlk);
+    p.nblk = cdiv(N, fwd_tokens_per_block(p.NT));
   } else {
     p.nblk = (int)std::min<int64_t>(512, std::max<int64_t>(1, (N + 15) / 16));
   }
@@ -777,12 +942,23 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+void launch_reduce(hipStream_t s, const float* ws, int nchunk, int64_t len, void* out, int out_dt) {
+  if (len % 4 == 0) {
+    const unsigned nb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (len / 4 + 63) / 64));
+    MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks<4>, dim3(nb), dim3(256), 0, s, ws, nchunk, len, out, out_dt);
+  } else {
+    const unsigned nb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (len + 63) / 64));
+    MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks<1>, dim3(nb), dim3(256), 0, s, ws, nchunk, len, out, out_dt);
+  }
+}
+
 template <int NT>
 void launch_fwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const i16x8* wp, const float* bias, int N, int H,
                      int E, int K, int64_t* idx, void* w, int w_dt, float* logits, float* lse, int* pc, float* pp,
                      float* pz) {
-  constexpr int U = NT == 1 ? 16 : (NT == 2 ? 8 : 4);
-  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_bf16<NT, U>), grid, dim3(256), 0, s, x, wp, bias, N, H, E, K, idx, w, w_dt,
+  constexpr int HS = fwd_hs(NT);
+  constexpr int U = fwd_u(NT);
+  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_bf16<NT, HS, U>), grid, dim3(256), 0, s, x, wp, bias, N, H, E, K, idx, w, w_dt,
                      logits, lse, pc, pp, pz);
 }
 
@@ -805,7 +981,8 @@ extern "C" size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int6
 
 extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias, int64_t N,
                               int64_t H, int64_t E, int64_t K, int64_t* idx_out, void* w_out, int w_dtype,
-                              float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out, void* workspace,
+                              float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out,
+                              float aux_coef, float z_coef, float* aux_out, float* z_out, void* workspace,
                               size_t ws_bytes, void* stream) {
   if (N < 0 || H <= 0 || E < 1 || E > kMaxE || K < 1 || K > E || K > kMaxK)
     return fail_arg("moe_router_fwd: bad shape N=%lld H=%lld E=%lld K=%lld (need 1<=K<=min(E,32), E<=256)",
@@ -842,7 +1019,7 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
     }
     if (int rc = check_launch("k_router_fwd_bf16")) return rc;
     MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(256), 0, s, pc, pp, pz, p.nblk, (int)N, (int)E, (int)K,
-                       cnt_out, stats_out);
+                       aux_coef, z_coef, cnt_out, stats_out, aux_out, z_out);
   } else {
     FwdPlan pg = p;
     if (p.mfma) {  // unaligned x: generic path needs its own block count
@@ -860,7 +1037,7 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
     MOE_LAUNCH("k_route_from_logits", k_route_from_logits, dim3(nblk), dim3(256), 0, s, logits_out, (int)N, (int)E, (int)K, tpb,
                        idx_out, w_out, w_dtype, lse_out, pc, pp, pz);
     MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(256), 0, s, pc, pp, pz, nblk, (int)N, (int)E, (int)K,
-                       cnt_out, stats_out);
+                       aux_coef, z_coef, cnt_out, stats_out, aux_out, z_out);
   }
   return check_launch("moe_router_fwd");
 }
@@ -889,7 +1066,7 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
   if (N == 0) {
     const int64_t len = H * E;
     // dwg = 0 when there are no tokens
-    MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks, dim3((unsigned)std::min<int64_t>(1024, (len + 255) / 256)), dim3(256), 0, s,
+    launch_reduce(s,
                        static_cast<const float*>(nullptr), 0, len, dwg_out, wg_dtype);
     return check_launch("moe_router_bwd");
   }
@@ -900,10 +1077,21 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
   float* wsdw = reinterpret_cast<float*>(ws + p.off_ws);
   const bool mfma = p.mfma && aligned16(x) && aligned16(dx_out);
   uint16_t* gb = mfma ? reinterpret_cast<uint16_t*>(ws + p.off_gb) : nullptr;
-  const unsigned gl_blocks = (unsigned)std::min<int64_t>(8192, (N + 3) / 4);
-  MOE_LAUNCH("k_router_glogits", k_router_glogits, dim3(gl_blocks), dim3(256), 0, s, logits, idx, grad_w, gw_dtype, cnt, grad_aux,
-                     grad_z, aux_coef, z_coef, (int)N, (int)E, (int)K, (int)(x_dtype == MOE_BF16), G, gb,
-                     p.EK * 32);
+  {
+    const int ekp = p.EK * 32;
+    const int rb = (int)(x_dtype == MOE_BF16);
+#define MOE_GLOG(LPT, EPL)                                                                                     \
+  MOE_LAUNCH("k_router_glogits", (k_router_glogits<LPT, EPL>),                                                 \
+             dim3((unsigned)std::min<int64_t>(4096, (N * LPT + 255) / 256)), dim3(256), 0, s, logits, idx,     \
+             grad_w, gw_dtype, cnt, grad_aux, grad_z, aux_coef, z_coef, (int)N, (int)E, (int)K, rb, G, gb, ekp)
+    if (E <= 8) MOE_GLOG(8, 1);
+    else if (E <= 16) MOE_GLOG(16, 1);
+    else if (E <= 32) MOE_GLOG(32, 1);
+    else if (E <= 64) MOE_GLOG(64, 1);
+    else if (E <= 128) MOE_GLOG(64, 2);
+    else MOE_GLOG(64, 4);
+#undef MOE_GLOG
+  }
   if (int rc = check_launch("k_router_glogits")) return rc;
   int nchunk = p.nchunk;
   if (mfma) {
@@ -932,7 +1120,7 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
     if (int rc = check_launch("k_router_dw_generic")) return rc;
   }
   const int64_t len = H * E;
-  MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks, dim3((unsigned)std::min<int64_t>(1024, (len + 255) / 256)), dim3(256), 0, s,
+  launch_reduce(s,
                      wsdw, nchunk, len, dwg_out, wg_dtype);
   return check_launch("moe_router_bwd");
 }

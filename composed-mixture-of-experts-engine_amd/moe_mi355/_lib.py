@@ -35,7 +35,8 @@ _SIGNATURES = {
     "moe_router_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
     "moe_router_fwd": (
         _I32,
-        [_P, _I32, _P, _I32, _P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _P, _P, _P, _SZ, _P],
+        [_P, _I32, _P, _I32, _P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _P, _P, _F32, _F32, _P, _P, _P, _SZ,
+         _P],
     ),
     "moe_router_bwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
     "moe_router_bwd": (

@@ -23,12 +23,16 @@ def router_forward(
     k: int,
     bias: Optional[torch.Tensor] = None,
     w_dtype: Optional[torch.dtype] = None,
+    aux_coef: float = 0.0,
+    z_coef: float = 0.0,
+    with_losses: bool = False,
 ) -> Tuple[torch.Tensor, ...]:
     """Fused router forward on the GPU.
 
     Returns ``(idx int64 [N,K], w [N,K] (w_dtype, default x.dtype), logits f32 [N,E],
-    lse f32 [N], cnt int64 [E], stats f32 [8+E])``; the stats layout is
-    documented in include/moe_mi355.h.
+    lse f32 [N], cnt int64 [E], stats f32 [8+E])``, followed by the 0-d tensors
+    ``aux = aux_coef * stats[1]`` and ``z = z_coef * stats[0]`` when
+    ``with_losses``; the stats layout is documented in include/moe_mi355.h.
     """
     dev = L.require_device(x, gate_w, bias)
     x = x.contiguous()
@@ -47,18 +51,28 @@ def router_forward(
     logits = torch.empty((N, E), dtype=torch.float32, device=dev)
     lse = torch.empty((N,), dtype=torch.float32, device=dev)
     cnt = torch.empty((E,), dtype=torch.int64, device=dev)
-    stats = torch.zeros((L.STATS_HEAD + E,), dtype=torch.float32, device=dev)
+    stats = torch.empty((L.STATS_HEAD + E,), dtype=torch.float32, device=dev)
+    aux = torch.empty((), dtype=torch.float32, device=dev) if with_losses else None
+    z = torch.empty((), dtype=torch.float32, device=dev) if with_losses else None
     if N == 0:
         cnt.zero_()
+        stats.zero_()
+        if with_losses:
+            aux.zero_()
+            z.zero_()
+            return idx, w, logits, lse, cnt, stats, aux, z
         return idx, w, logits, lse, cnt, stats
     nbytes = lib.moe_router_fwd_workspace(N, H, E, k, xdt, wdt)
     ws = L.workspace(nbytes, dev)
     rc = lib.moe_router_fwd(
         x.data_ptr(), xdt, gate_w.data_ptr(), wdt, L.ptr(bias), N, H, E, k,
         idx.data_ptr(), w.data_ptr(), odt, logits.data_ptr(), lse.data_ptr(),
-        cnt.data_ptr(), stats.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+        cnt.data_ptr(), stats.data_ptr(), float(aux_coef), float(z_coef), L.ptr(aux), L.ptr(z),
+        ws.data_ptr(), nbytes, L.stream_of(dev),
     )
     L.check(rc, "moe_router_fwd")
+    if with_losses:
+        return idx, w, logits, lse, cnt, stats, aux, z
     return idx, w, logits, lse, cnt, stats
 
 

@@ -39,9 +39,9 @@ class RouterCore(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, gate_w, k: int, aux_coef: float, z_coef: float, bias: Optional[torch.Tensor] = None):
-        idx, w, logits, lse, cnt, stats = ops.router_forward(x, gate_w, k, bias)
-        aux = stats[STAT_AUX] * float(aux_coef)
-        z = stats[STAT_Z] * float(z_coef)
+        idx, w, logits, lse, cnt, stats, aux, z = ops.router_forward(
+            x, gate_w, k, bias, aux_coef=aux_coef, z_coef=z_coef, with_losses=True
+        )
         ctx.save_for_backward(x, gate_w, logits, idx, cnt)
         ctx.aux_coef = float(aux_coef)
         ctx.z_coef = float(z_coef)

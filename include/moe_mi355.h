@@ -79,6 +79,8 @@ int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
  *   idx_out  [N, K]  int64            w_out [N, K] w_dtype
  *   logits_out [N, E] f32             lse_out [N] f32
  *   cnt_out  [E] int64                stats_out [MOE_STATS_HEAD + E] f32
+ *   aux_out  [1] f32 or NULL: aux_coef * stats[1] (load-balance loss)
+ *   z_out    [1] f32 or NULL: z_coef * stats[0]   (z-loss)
  * Limits: 1 <= K <= min(E, 32), 1 <= E <= 256.
  * ---------------------------------------------------------------------- */
 size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
@@ -86,6 +88,7 @@ int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, con
                    int64_t N, int64_t H, int64_t E, int64_t K,
                    int64_t* idx_out, void* w_out, int w_dtype,
                    float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out,
+                   float aux_coef, float z_coef, float* aux_out, float* z_out,
                    void* workspace, size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------------------

@@ -18,19 +18,22 @@ def say(*a) -> None:
     print(*a, file=sys.stderr, flush=True)
 
 
-def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
-    """max|a-b| / max|b| (max-norm relative error), float64 on the CPU."""
+def rel_err(a: torch.Tensor, b: torch.Tensor, floor: float = 0.0) -> float:
+    """max|a-b| / max(max|b|, floor) (max-norm relative error), float64 on the CPU.
+
+    ``floor`` keeps the measure meaningful when the exact result is zero up to
+    rounding (e.g. K=1 routing, where the combine weight is identically 1)."""
     a = a.detach().to("cpu", torch.float64)
     b = b.detach().to("cpu", torch.float64)
-    den = b.abs().max().item()
+    den = max(b.abs().max().item() if b.numel() else 0.0, floor)
     if den == 0.0:
-        return a.abs().max().item()
+        return a.abs().max().item() if a.numel() else 0.0
     return (a - b).abs().max().item() / den
 
 
-def assert_rel(a: torch.Tensor, b: torch.Tensor, tol: float, what: str = "") -> None:
+def assert_rel(a: torch.Tensor, b: torch.Tensor, tol: float, what: str = "", floor: float = 0.0) -> None:
     assert a.shape == b.shape, f"{what}: shape {tuple(a.shape)} vs {tuple(b.shape)}"
-    e = rel_err(a, b)
+    e = rel_err(a, b, floor)
     assert e <= tol, f"{what}: max-norm relative error {e:.3e} > {tol:.1e}"
 
 

@@ -45,14 +45,14 @@ def test_version_string():
 def test_router_fwd_rejects_bad_shapes_without_gpu():
     lib = _lib.load()
     # K > E
-    rc = lib.moe_router_fwd(None, 1, None, 1, None, 16, 64, 4, 8, None, None, 1, None, None, None, None, None, 0, None)
+    rc = lib.moe_router_fwd(None, 1, None, 1, None, 16, 64, 4, 8, None, None, 1, None, None, None, None, 0.0, 0.0, None, None, None, 0, None)
     assert rc == -1
     assert "bad shape" in _lib.last_error()
     # unsupported dtype code
-    rc = lib.moe_router_fwd(None, 7, None, 1, None, 16, 64, 8, 2, None, None, 1, None, None, None, None, None, 0, None)
+    rc = lib.moe_router_fwd(None, 7, None, 1, None, 16, 64, 8, 2, None, None, 1, None, None, None, None, 0.0, 0.0, None, None, None, 0, None)
     assert rc == -1 and "dtype" in _lib.last_error()
     # null pointers
-    rc = lib.moe_router_fwd(None, 1, None, 1, None, 16, 64, 8, 2, None, None, 1, None, None, None, None, None, 0, None)
+    rc = lib.moe_router_fwd(None, 1, None, 1, None, 16, 64, 8, 2, None, None, 1, None, None, None, None, 0.0, 0.0, None, None, None, 0, None)
     assert rc == -1 and "null" in _lib.last_error()
 
 
@@ -73,7 +73,7 @@ def test_workspace_queries_are_pure_host_arithmetic():
 
 def test_check_raises_value_error_for_argument_codes():
     lib = _lib.load()
-    rc = lib.moe_router_fwd(None, 1, None, 1, None, 16, 64, 4, 8, None, None, 1, None, None, None, None, None, 0, None)
+    rc = lib.moe_router_fwd(None, 1, None, 1, None, 16, 64, 4, 8, None, None, 1, None, None, None, None, 0.0, 0.0, None, None, None, 0, None)
     with pytest.raises(ValueError):
         _lib.check(rc, "moe_router_fwd")
 

@@ -117,8 +117,9 @@ def test_router_backward_parity(shape, losses):
     torch.cuda.synchronize()
     ref = OR.router_full(x, w, K, grad_w=gw, alpha=alpha, beta=beta, idx_override=idx.cpu())
     tol = TOL[x.dtype]
-    assert_rel(xd_.grad, ref["dX"], tol, "dX")
-    assert_rel(wd_.grad, ref["dW"], tol if w.dtype == torch.float32 or x.dtype == torch.float32 else tol, "dW")
+    # gradients of order 1e-2 here; the floor only matters where the exact gradient vanishes (K=1)
+    assert_rel(xd_.grad, ref["dX"], tol, "dX", floor=1e-4)
+    assert_rel(wd_.grad, ref["dW"], tol, "dW", floor=1e-4)
     if losses:
         assert abs(aux.item() - float(ref["aux"])) <= 1e-5 * float(ref["aux"])
         assert abs(z.item() - float(ref["z"])) <= 1e-5 * float(ref["z"])
