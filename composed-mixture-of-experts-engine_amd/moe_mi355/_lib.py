@@ -43,6 +43,18 @@ _SIGNATURES = {
         _I32,
         [_P, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _F32, _F32, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
     ),
+    "moe_plan_workspace": (_SZ, [_I64, _I64, _I64]),
+    "moe_plan": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "moe_permute": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "moe_combine": (_I32, [_P, _I32, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "moe_combine_bwd": (_I32, [_P, _P, _I32, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "moe_unpermute_sum": (_I32, [_P, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "moe_swiglu_workspace": (_SZ, [_I64]),
+    "moe_swiglu_fwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "moe_swiglu_bwd": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
 }
 
 _lock = threading.Lock()

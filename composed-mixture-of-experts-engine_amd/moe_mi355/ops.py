@@ -123,3 +123,164 @@ def router_backward(
     )
     L.check(rc, "moe_router_bwd")
     return dx, dw
+
+
+# ---------------------------------------------------------------------------
+# Dispatch planner, permute, combine
+# ---------------------------------------------------------------------------
+LAYOUT_REFERENCE = 0
+LAYOUT_ROUTED = 1
+
+
+class Plan:
+    """Device-side dispatch plan (every field is a tensor on the GPU).
+
+    ``drop`` [N,K] bool or None, ``row_slot`` [N*K] int32, ``slot_row`` [N*K]
+    int32, ``offsets`` [E+1] int32, ``ndrop`` [1] int32; ``rows`` = N*K is the
+    allocated row count (rows past offsets[E] are not computed).
+    """
+
+    __slots__ = ("drop", "row_slot", "slot_row", "offsets", "ndrop", "N", "K", "E", "layout")
+
+    def __init__(self, drop, row_slot, slot_row, offsets, ndrop, N, K, E, layout):
+        self.drop, self.row_slot, self.slot_row, self.offsets, self.ndrop = drop, row_slot, slot_row, offsets, ndrop
+        self.N, self.K, self.E, self.layout = N, K, E, layout
+
+    @property
+    def rows(self) -> int:
+        return self.N * self.K
+
+    def drop_u8(self):
+        return None if self.drop is None else self.drop.view(torch.uint8)
+
+
+def plan(idx: torch.Tensor, num_experts: int, capacity: int = -1, layout: int = LAYOUT_REFERENCE) -> Plan:
+    """Build the dispatch plan from the router's top-k indices (no host sync)."""
+    dev = L.require_device(idx)
+    idx = idx.contiguous()
+    if idx.dtype != torch.int64:
+        idx = idx.long()
+    N, K = idx.shape
+    E = int(num_experts)
+    lib = L.load()
+    drop = torch.empty((N, K), dtype=torch.bool, device=dev) if capacity >= 0 else None
+    M = N * K
+    row_slot = torch.empty((max(M, 1),), dtype=torch.int32, device=dev)
+    slot_row = torch.empty((max(M, 1),), dtype=torch.int32, device=dev)
+    offsets = torch.empty((E + 1,), dtype=torch.int32, device=dev)
+    ndrop = torch.zeros((1,), dtype=torch.int32, device=dev) if M == 0 else torch.empty((1,), dtype=torch.int32,
+                                                                                         device=dev)
+    nbytes = lib.moe_plan_workspace(N, K, E)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_plan(
+        idx.data_ptr(), N, K, E, int(capacity), int(layout),
+        L.ptr(drop), row_slot.data_ptr(), slot_row.data_ptr(), offsets.data_ptr(), ndrop.data_ptr(),
+        ws.data_ptr(), nbytes, L.stream_of(dev),
+    )
+    L.check(rc, "moe_plan")
+    return Plan(drop, row_slot[:M], slot_row[:M], offsets, ndrop, N, K, E, layout)
+
+
+def permute(x: torch.Tensor, p: Plan) -> torch.Tensor:
+    """xp [N*K, H]: row r holds x[row_slot[r] // K] (rows past offsets[E] are left unwritten)."""
+    dev = L.require_device(x)
+    x = x.contiguous()
+    H = x.shape[1]
+    xp = torch.empty((p.rows, H), dtype=x.dtype, device=dev)
+    if p.rows == 0:
+        return xp
+    rc = L.load().moe_permute(x.data_ptr(), H * x.element_size(), p.row_slot.data_ptr(), p.offsets.data_ptr(),
+                              p.E, p.K, p.rows, xp.data_ptr(), L.stream_of(dev))
+    L.check(rc, "moe_permute")
+    return xp
+
+
+def combine(y: torch.Tensor, w: torch.Tensor, p: Plan) -> torch.Tensor:
+    dev = L.require_device(y, w)
+    y = y.contiguous()
+    w = w.contiguous()
+    H = y.shape[1]
+    out = torch.empty((p.N, H), dtype=y.dtype, device=dev)
+    rc = L.load().moe_combine(y.data_ptr(), L.dtype_code(y.dtype), w.data_ptr(), L.dtype_code(w.dtype),
+                              L.ptr(p.drop_u8()), p.slot_row.data_ptr(), p.offsets.data_ptr(), p.N, p.K, H, p.E,
+                              out.data_ptr(), L.stream_of(dev))
+    L.check(rc, "moe_combine")
+    return out
+
+
+def combine_backward(dout: torch.Tensor, y: torch.Tensor, w: torch.Tensor, p: Plan, need_dw: bool = True,
+                     zero_tail: bool = False):
+    """Returns (dy [rows, H], dw [N, K] or None).  Rows past offsets[E] of dy are
+    left unwritten unless ``zero_tail`` (then the whole buffer starts at zero)."""
+    dev = L.require_device(dout, y, w)
+    dout = dout.contiguous()
+    H = y.shape[1]
+    dy = torch.zeros_like(y) if zero_tail else torch.empty_like(y)
+    dw = torch.empty((p.N, p.K), dtype=w.dtype, device=dev) if need_dw else None
+    rc = L.load().moe_combine_bwd(dout.data_ptr(), y.data_ptr(), L.dtype_code(y.dtype), w.contiguous().data_ptr(),
+                                  L.dtype_code(w.dtype), L.ptr(p.drop_u8()), p.slot_row.data_ptr(),
+                                  p.offsets.data_ptr(), p.N, p.K, H, p.E, dy.data_ptr(), L.ptr(dw),
+                                  L.stream_of(dev))
+    L.check(rc, "moe_combine_bwd")
+    return dy, dw
+
+
+def unpermute_sum(dxp: torch.Tensor, p: Plan, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
+    dev = L.require_device(dxp, addend)
+    H = dxp.shape[1]
+    dx = torch.empty((p.N, H), dtype=dxp.dtype, device=dev)
+    if addend is not None:
+        addend = addend.contiguous()
+    rc = L.load().moe_unpermute_sum(dxp.contiguous().data_ptr(), L.ptr(addend), L.dtype_code(dxp.dtype),
+                                    p.slot_row.data_ptr(), p.offsets.data_ptr(), p.N, p.K, H, p.E, dx.data_ptr(),
+                                    L.stream_of(dev))
+    L.check(rc, "moe_unpermute_sum")
+    return dx
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU grouped GEMM (bf16)
+# ---------------------------------------------------------------------------
+def swiglu_forward(xp: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                   offsets: torch.Tensor):
+    """xp [R,H]; w_gate/w_up [E,F,H]; w_down [E,H,F] (bf16, contiguous) -> (act [R,F], hgu [R,2F], y [R,H])."""
+    dev = L.require_device(xp, w_gate, w_up, w_down, offsets)
+    for t in (xp, w_gate, w_up, w_down):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("swiglu_forward: the grouped GEMM runs on bfloat16 tensors")
+        if not t.is_contiguous():
+            raise ValueError("swiglu_forward: tensors must be contiguous")
+    R, H = xp.shape
+    E, F, _ = w_gate.shape
+    act = torch.empty((R, F), dtype=xp.dtype, device=dev)
+    hgu = torch.empty((R, 2 * F), dtype=xp.dtype, device=dev)
+    y = torch.empty((R, H), dtype=xp.dtype, device=dev)
+    lib = L.load()
+    nbytes = lib.moe_swiglu_workspace(E)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_swiglu_fwd(xp.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(),
+                            offsets.data_ptr(), R, H, F, E, act.data_ptr(), hgu.data_ptr(), y.data_ptr(),
+                            ws.data_ptr(), nbytes, L.stream_of(dev))
+    L.check(rc, "moe_swiglu_fwd")
+    return act, hgu, y
+
+
+def swiglu_backward(dy, xp, act, hgu, w_gate, w_up, w_down, offsets):
+    """-> (dxp [R,H], dw_gate [E,F,H], dw_up [E,F,H], dw_down [E,H,F])."""
+    dev = L.require_device(dy, xp, act, hgu, w_gate, w_up, w_down, offsets)
+    R, H = xp.shape
+    E, F, _ = w_gate.shape
+    dh = torch.empty((R, 2 * F), dtype=xp.dtype, device=dev)
+    dxp = torch.empty((R, H), dtype=xp.dtype, device=dev)
+    dwg = torch.empty_like(w_gate)
+    dwu = torch.empty_like(w_up)
+    dwd = torch.empty_like(w_down)
+    lib = L.load()
+    nbytes = lib.moe_swiglu_workspace(E)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_swiglu_bwd(dy.contiguous().data_ptr(), xp.data_ptr(), act.data_ptr(), hgu.data_ptr(),
+                            w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), offsets.data_ptr(), R, H, F, E,
+                            dh.data_ptr(), dxp.data_ptr(), dwg.data_ptr(), dwu.data_ptr(), dwd.data_ptr(),
+                            ws.data_ptr(), nbytes, L.stream_of(dev))
+    L.check(rc, "moe_swiglu_bwd")
+    return dxp, dwg, dwu, dwd

@@ -1,0 +1,254 @@
+"""MoE layer with the reference's API, on the gfx950 kernels.
+
+Mirrors ``moe-engine/pkg/distributed/moe_layer.py``:
+
+* ``DistributedMoELayer(hidden_dim, ffn_dim, num_experts, top_k, topology,
+  capacity_factor=1.25, capacity_dropping=False, dtype=torch.float32)``,
+  ``forward([B,S,H] | [N,H]) -> same shape`` (L:206-360);
+* ``compute_capacity_drop_mask(idx, num_experts, capacity) -> Bool[N,K]``
+  and ``_cumcount(groups) -> Long[n]`` (L:64-155);
+* ``_SwiGLUExpert`` (L:166-198) and the attributes ``router``, ``experts``,
+  ``local_expert_ids``, ``last_{dispatch,combine,expert_compute}_ms``,
+  ``last_overlap_ratio``, ``last_dropped_token_fraction``, ``_expert_to_rank``.
+
+Forward pipeline, all on the GPU with no host synchronisation:
+router kernel -> planner kernels (capacity drops, row layout) -> permute ->
+SwiGLU grouped GEMM -> weighted combine.  The backward is the fused mirror
+(combine-bwd, grouped GEMM backward, permute-bwd) plus the router backward.
+
+Row layout (``layout`` argument, new):
+* ``"reference"`` (default) reproduces the reference exactly: tokens are
+  stable-sorted by their first choice, repeated K times, and the [N*K, H]
+  buffer is cut into E equal chunks, chunk i going to expert i whatever the
+  router chose (L:317-337); rows past E*chunk contribute zero.
+* ``"routed"``: slot (t, k) goes to expert idx[t, k]; dropped slots get no row.
+
+Expert weights are held stacked -- ``w_gate`` / ``w_up`` [E, F, H] and
+``w_down`` [E, H, F] -- so one grouped GEMM reads them; ``experts[i]`` exposes
+expert i's slices as ``w_gate.weight`` etc., and ``state_dict`` /
+``load_state_dict`` use the reference's per-expert keys
+(``experts.{i}.w_gate.weight``).  Assigning a different ModuleList to
+``experts`` (the reference's extension point) switches the layer to calling
+those modules per expert between the dispatch and combine kernels.  bf16 uses
+the fused HIP grouped GEMM; other dtypes call the expert modules per expert.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from moe_mi355 import ops
+from moe_mi355.layer import CombineFn, ExpertsFn, PermuteFn
+from pkg.kernels.moe_router import MoERouter
+
+__all__ = ["DistributedMoELayer", "compute_capacity_drop_mask", "_cumcount"]
+
+_LAYOUTS = {"reference": ops.LAYOUT_REFERENCE, "routed": ops.LAYOUT_ROUTED}
+
+
+def _cumcount(groups: torch.Tensor) -> torch.Tensor:
+    """Each element's 0-based position among earlier elements of its group (L:64-115).
+
+    Runs the planner's stable-grouping kernel (one column of K=1)."""
+    n = groups.shape[0]
+    if n == 0:
+        return torch.empty(0, dtype=torch.long, device=groups.device)
+    g = groups.reshape(n, 1).long()
+    g = g - g.min()
+    E = int(g.max().item()) + 1
+    # rank of each element within its key = position in the stable sort minus the key's offset
+    p = ops.plan(g, max(E, 1), capacity=-1, layout=ops.LAYOUT_ROUTED)
+    pos = p.slot_row.long()
+    return pos - p.offsets.long()[g.reshape(-1)]
+
+
+def compute_capacity_drop_mask(idx: torch.Tensor, num_experts: int, capacity: int) -> torch.Tensor:
+    """``drop[t, k] = cumcount(idx[:, k])[t] >= capacity`` per column (L:118-155)."""
+    N, K = idx.shape
+    if N == 0:
+        return torch.zeros(N, K, dtype=torch.bool, device=idx.device)
+    # any integer group ids are valid here, as in the reference (one host read of the range)
+    lo, hi = (int(v) for v in torch.stack([idx.min(), idx.max()]).tolist())
+    if lo < 0 or hi >= num_experts:
+        idx = idx - lo
+        num_experts = hi - lo + 1
+    # capacity < 0 drops every slot (position >= capacity always holds)
+    p = ops.plan(idx, num_experts, capacity=max(int(capacity), 0), layout=ops.LAYOUT_REFERENCE)
+    if capacity < 0:
+        return torch.ones(N, K, dtype=torch.bool, device=idx.device)
+    return p.drop
+
+
+class _ExpertWeight(nn.Module):
+    """``.weight`` of one expert projection: a view of the layer's stacked tensor."""
+
+    def __init__(self, owner_ref, name: str, index: int):
+        super().__init__()
+        object.__setattr__(self, "_owner", owner_ref)
+        object.__setattr__(self, "_name", name)
+        object.__setattr__(self, "_index", index)
+
+    @property
+    def weight(self) -> torch.Tensor:
+        return getattr(self._owner(), self._name)[self._index]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(x, self.weight)
+
+
+class _SwiGLUExpert(nn.Module):
+    """``w_down(silu(w_gate(x)) * w_up(x))`` (L:166-198) over expert ``index``'s slices."""
+
+    def __init__(self, owner_ref, index: int):
+        super().__init__()
+        self.w_gate = _ExpertWeight(owner_ref, "w_gate", index)
+        self.w_up = _ExpertWeight(owner_ref, "w_up", index)
+        self.w_down = _ExpertWeight(owner_ref, "w_down", index)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+
+
+class DistributedMoELayer(nn.Module):
+    def __init__(
+        self,
+        hidden_dim: int,
+        ffn_dim: int,
+        num_experts: int,
+        top_k: int,
+        topology,
+        capacity_factor: float = 1.25,
+        capacity_dropping: bool = False,
+        dtype: torch.dtype = torch.float32,
+        layout: str = "reference",
+        aux_loss_coef: float = 0.0,
+        z_loss_coef: float = 0.0,
+        check_numerics: bool = True,
+    ):
+        super().__init__()
+        if getattr(topology, "ep_size", 1) != 1 or getattr(topology, "tp_size", 1) != 1:
+            raise NotImplementedError("this build runs one GPU's experts; ep_size/tp_size > 1 are out of scope")
+        if layout not in _LAYOUTS:
+            raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {layout!r}")
+        self.hidden_dim = hidden_dim
+        self.ffn_dim = ffn_dim
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.topology = topology
+        self.capacity_factor = capacity_factor
+        self.capacity_dropping = capacity_dropping
+        self.layout = layout
+        self.check_numerics = check_numerics
+        self.local_expert_ids: List[int] = topology.experts_on_this_rank(num_experts)
+        dev = getattr(topology, "device", None)
+        E = len(self.local_expert_ids)
+        # nn.Linear-style init N(0, 1/sqrt(in)) per projection (tensor_parallel.py L:109, L:187)
+        self.w_gate = nn.Parameter(torch.empty(E, ffn_dim, hidden_dim, device=dev, dtype=dtype))
+        self.w_up = nn.Parameter(torch.empty(E, ffn_dim, hidden_dim, device=dev, dtype=dtype))
+        self.w_down = nn.Parameter(torch.empty(E, hidden_dim, ffn_dim, device=dev, dtype=dtype))
+        nn.init.normal_(self.w_gate, mean=0.0, std=1.0 / math.sqrt(hidden_dim))
+        nn.init.normal_(self.w_up, mean=0.0, std=1.0 / math.sqrt(hidden_dim))
+        nn.init.normal_(self.w_down, mean=0.0, std=1.0 / math.sqrt(ffn_dim))
+        import weakref
+
+        ref = weakref.ref(self)
+        self.experts = nn.ModuleList([_SwiGLUExpert(ref, i) for i in range(E)])
+        self.router = MoERouter(hidden_dim, num_experts, top_k, dtype=dtype, aux_loss_coef=aux_loss_coef,
+                                z_loss_coef=z_loss_coef, sync_profile=check_numerics)
+        if dev is not None:
+            self.router.to(dev)
+        self.last_dispatch_ms: float = 0.0
+        self.last_combine_ms: float = 0.0
+        self.last_expert_compute_ms: float = 0.0
+        self.last_overlap_ratio: float = 0.0
+        self.last_plan: Optional[ops.Plan] = None
+        self._register_state_dict_hook(DistributedMoELayer._to_reference_keys)
+        self._register_load_state_dict_pre_hook(DistributedMoELayer._from_reference_keys, with_module=True)
+
+    # ---- state_dict in the reference's per-expert key format ----
+    @staticmethod
+    def _to_reference_keys(module, state_dict, prefix, local_metadata):
+        for name in ("w_gate", "w_up", "w_down"):
+            key = prefix + name
+            if key in state_dict:
+                stacked = state_dict.pop(key)
+                for i in range(stacked.shape[0]):
+                    state_dict[f"{prefix}experts.{i}.{name}.weight"] = stacked[i]
+        return state_dict
+
+    @staticmethod
+    def _from_reference_keys(module, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                             error_msgs):
+        for name in ("w_gate", "w_up", "w_down"):
+            keys = [f"{prefix}experts.{i}.{name}.weight" for i in range(getattr(module, name).shape[0])]
+            if all(k in state_dict for k in keys):
+                state_dict[prefix + name] = torch.stack([state_dict.pop(k) for k in keys])
+
+    @property
+    def last_dropped_token_fraction(self) -> float:
+        """Fraction of (token, k) slots dropped by capacity in the last forward (reads the device count)."""
+        p = self.last_plan
+        if p is None or not self.capacity_dropping or p.rows == 0:
+            return 0.0
+        return float(p.ndrop.item()) / float(p.rows)
+
+    def extra_repr(self) -> str:
+        return (
+            f"hidden={self.hidden_dim}, num_experts={self.num_experts}, top_k={self.top_k}, "
+            f"local_experts={len(self.local_expert_ids)}, ep_size=1, layout={self.layout}"
+        )
+
+    def _fused(self) -> bool:
+        return (
+            self.w_gate.dtype == torch.bfloat16
+            and all(type(m) is _SwiGLUExpert and m.w_gate._owner() is self for m in self.experts)
+            and len(self.experts) == self.num_experts
+        )
+
+    def forward(self, tokens: torch.Tensor) -> torch.Tensor:
+        original_shape = tokens.shape
+        if tokens.dim() not in (2, 3):
+            raise ValueError(f"tokens must be rank 2 or 3, got {tokens.dim()}")
+        H = tokens.shape[-1]
+        flat = tokens.reshape(-1, H)
+        N = flat.shape[0]
+        idx, weights, _cnt = self.router(flat)
+        capacity = (
+            math.ceil(self.capacity_factor * N * self.top_k / self.num_experts) if self.capacity_dropping else -1
+        )
+        p = ops.plan(idx, self.num_experts, capacity=capacity, layout=_LAYOUTS[self.layout])
+        self.last_plan = p
+        if self._fused():
+            out = ExpertsFn.apply(flat, weights, self.w_gate, self.w_up, self.w_down, p)
+        else:
+            out = self._forward_per_expert(flat, weights, p)
+        if self.check_numerics:
+            assert not torch.isnan(out).any(), (
+                "NaN detected in DistributedMoELayer output after combine step. "
+                "Check expert FFN numerics and router weights."
+            )
+        return out.reshape(original_shape)
+
+    def _forward_per_expert(self, flat: torch.Tensor, weights: torch.Tensor, p: ops.Plan) -> torch.Tensor:
+        """Dispatch/combine kernels around per-expert module calls (custom experts, non-bf16 dtypes)."""
+        xp = PermuteFn.apply(flat, p)
+        offs = p.offsets.tolist()  # segment bounds for the per-expert calls
+        parts = []
+        for i, expert in enumerate(self.experts):
+            lo, hi = offs[i], offs[i + 1]
+            if lo < hi:
+                parts.append(expert(xp[lo:hi]))
+        tail = p.rows - offs[len(self.experts)]
+        if tail > 0:
+            parts.append(xp.new_zeros((tail, xp.shape[1])))
+        y = torch.cat(parts, 0) if parts else xp.new_zeros(xp.shape)
+        return CombineFn.apply(y.contiguous(), weights, p)
+
+    def _expert_to_rank(self, expert_ids: torch.Tensor) -> torch.Tensor:
+        """Every expert lives on this (single) rank (reference L:362-389 at ep_size=1)."""
+        return torch.zeros_like(expert_ids, dtype=torch.long)

@@ -171,6 +171,7 @@ class MoERouter(torch.nn.Module):
         self.last_aux_loss: Optional[torch.Tensor] = None
         self.last_z_loss: Optional[torch.Tensor] = None
         self.last_stats: Optional[torch.Tensor] = None
+        self.last_stats_host: Optional[torch.Tensor] = None
 
     def forward(self, tokens: torch.Tensor, force_reference: bool = False):
         """Returns ``(topk_idx [N,K] int64, topk_w [N,K] tokens.dtype, dispatch_cnt [E] int64)``."""
@@ -199,6 +200,7 @@ class MoERouter(torch.nn.Module):
 
         if self.sync_profile:
             head = stats[:8].to("cpu")  # the single device->host copy of this forward
+            self.last_stats_host = head
             total = int(round(float(head[STAT_CNT_TOTAL])))
             expected_total = N * self.top_k
             assert total == expected_total, (

@@ -115,6 +115,82 @@ int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg_dtype,
                    void* dx_out, void* dwg_out,
                    void* workspace, size_t ws_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Dispatch planner.  From the router's idx [N, K] (int64) builds, on the
+ * device and deterministically:
+ *   drop_out [N, K] uint8  per-top-k-column capacity drops: slot (t, k) is
+ *            dropped when t is at position >= capacity among the tokens whose
+ *            k-th choice is the same expert (capacity < 0: no dropping,
+ *            drop_out may be NULL);
+ *   row_slot [N*K] int32   slot t*K+k held by each permuted row (-1: none);
+ *   slot_row [N*K] int32   row of each slot (-1: the slot has no row);
+ *   offsets  [E+1] int32   rows of expert e are [offsets[e], offsets[e+1]);
+ *            rows >= offsets[E] are never computed;
+ *   ndrop    [1] int32     number of dropped slots.
+ * layout 0 ("reference") reproduces DistributedMoELayer.forward at ep=1: rows
+ * are the tokens stable-sorted by their first choice, each repeated K times,
+ * cut into E equal chunks of max(1, N*K / E) rows; dropped slots keep their
+ * row and get zero weight.  layout 1 ("routed"): slot (t, k) goes to expert
+ * idx[t, k], rows grouped by expert in slot order, dropped slots get no row.
+ *
+ * Replaces _cumcount and compute_capacity_drop_mask
+ * (pkg/distributed/moe_layer.py L:64-115, L:118-155), the capacity rule of
+ * L:300-306, the sort/repeat of L:317-319 and the chunking of L:327-336.
+ * ---------------------------------------------------------------------- */
+size_t moe_plan_workspace(int64_t N, int64_t K, int64_t E);
+int moe_plan(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout,
+             uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
+             void* workspace, size_t ws_bytes, void* stream);
+
+/* Permute (dispatch): xp[r] = x[row_slot[r] / K] for r < offsets[E]; rows are
+ * row_bytes long (a multiple of 16).  Replaces flat[sort_order]
+ * .repeat_interleave(K) (pkg/distributed/moe_layer.py L:318-319). */
+int moe_permute(const void* x, int64_t row_bytes, const int32_t* row_slot, const int32_t* offsets,
+                int64_t E, int64_t K, int64_t R, void* xp, void* stream);
+
+/* Weighted combine: out[t] = sum_k w[t,k] y[slot_row[t*K+k]] over slots that
+ * have a computed row and are not dropped (drop may be NULL); fp32 sums, one
+ * write per token.  Replaces the weighted scatter of
+ * pkg/distributed/moe_layer.py L:347-353 (and the masked_fill of L:305). */
+int moe_combine(const void* y, int dtype, const void* w, int w_dtype, const uint8_t* drop,
+                const int32_t* slot_row, const int32_t* offsets, int64_t N, int64_t K, int64_t H, int64_t E,
+                void* out, void* stream);
+
+/* Combine backward: dy[row] = w'[t,k] dout[t]; dw[t,k] = <dout[t], y[row]>
+ * (0 for dropped slots and slots without a computed row).  The autograd
+ * backward of L:347-353 in the reference. */
+int moe_combine_bwd(const void* dout, const void* y, int dtype, const void* w, int w_dtype, const uint8_t* drop,
+                    const int32_t* slot_row, const int32_t* offsets, int64_t N, int64_t K, int64_t H, int64_t E,
+                    void* dy, void* dw, void* stream);
+
+/* Permute backward: dx[t] = addend[t] (NULL = 0) + sum_k dxp[slot_row[t*K+k]]
+ * over computed rows.  The autograd backward of L:318-319. */
+int moe_unpermute_sum(const void* dxp, const void* addend, int dtype, const int32_t* slot_row,
+                      const int32_t* offsets, int64_t N, int64_t K, int64_t H, int64_t E, void* dx, void* stream);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU expert grouped GEMM, bf16 (fp32 accumulate).  For the rows of each
+ * expert segment:  act = silu(xp Wg_e^T) * (xp Wu_e^T),  y = act Wd_e^T,
+ * with w_gate / w_up [E, F, H] and w_down [E, H, F] (the reference's
+ * nn.Linear [out, in] layout per expert).  hgu [R, 2F] keeps the two
+ * pre-activations [g | u] for the backward.  Replaces the expert loop of
+ * pkg/distributed/moe_layer.py L:326-337 over _SwiGLUExpert.forward
+ * (L:197-198; F.linear at tp=1, pkg/distributed/tensor_parallel.py
+ * L:117-121, L:195-199).
+ *
+ * Backward: dh [R, 2F] = [dg | du], dxp [R, H], and the weight gradients
+ * dw_gate / dw_up [E, F, H], dw_down [E, H, F] (experts without rows get 0).
+ * Limits: H % 8 == 0, F % 32 == 0, E <= 1024.
+ * ---------------------------------------------------------------------- */
+size_t moe_swiglu_workspace(int64_t E);
+int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_up, const void* w_down,
+                   const int32_t* offsets, int64_t R, int64_t H, int64_t F, int64_t E,
+                   void* act, void* hgu, void* y, void* workspace, size_t ws_bytes, void* stream);
+int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* hgu, const void* w_gate,
+                   const void* w_up, const void* w_down, const int32_t* offsets, int64_t R, int64_t H,
+                   int64_t F, int64_t E, void* dh, void* dxp, void* dw_gate, void* dw_up, void* dw_down,
+                   void* workspace, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
