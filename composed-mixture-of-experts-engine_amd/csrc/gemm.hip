@@ -2,14 +2,18 @@
 //
 // One kernel template covers the six products of the expert FFN forward and
 // backward.  Each computes C[m, n] = sum_k A[m, k] B[n, k] on
-// v_mfma_f32_32x32x16_bf16 with 128x128x64 block tiles, 4 waves of 64x64, a
-// double-buffered LDS pipeline (k-contiguous rows, 16-byte fragment reads)
-// and a register stage for the next k-tile's global loads.
+// v_mfma_f32_32x32x16_bf16 with 256x256 block tiles (8 waves of 128x64) and
+// a 4-stage LDS ring of 32-wide k slices filled by LDS-DMA
+// (global_load_lds_dwordx4) three stages ahead, so no operand passes through
+// VGPRs and each load has three compute slices to land.  Blocks are numbered
+// so that each XCD (blockIdx mod 8) runs a contiguous range of logical tiles:
+// tiles that share a weight panel stay in one L2.
 //
-//   operand mode 0 ("rows"): element (i, k) at P[i*ld + k]  (k contiguous,
-//                            copied to LDS with 16-byte stores)
-//   operand mode 1 ("cols"): element (i, k) at P[k*ld + i]  (i contiguous,
-//                            transposed into LDS with 2-byte stores)
+//   operand mode 0 ("rows"): element (i, k) at P[i*ld + k]  (k contiguous);
+//                            MFMA fragments are 16-byte LDS reads
+//   operand mode 1 ("cols"): element (i, k) at P[k*ld + i]  (i contiguous);
+//                            the tile keeps that layout in LDS and fragments are
+//                            read with the transposing ds_read_b64_tr_b16
 //   GROUP 0 (row-grouped): M = rows of one expert's segment
 //            [offsets[e], offsets[e+1]); B is that expert's weight.  Tiles are
 //            enumerated from a per-expert tile prefix so imbalanced segments
@@ -40,7 +44,7 @@ struct GemmArgs {
   const uint16_t* A;   // A operand source
   int64_t lda;
   const uint16_t* B;   // B operand source (first half when b_split > 0)
-  const uint16_t* B2;  // second B source: used for B index >= b_split (k for cols, n for EPI1)
+  const uint16_t* B2;  // second B source: B index >= b_split (k for cols mode) / up rows (EPI1)
   int64_t ldb;
   int64_t b_estride;   // per-expert stride of B / B2 (row-grouped), 0 otherwise
   int b_split;
@@ -52,233 +56,312 @@ struct GemmArgs {
   const uint16_t* X;   // EPI2: hgu
   int F;               // EPI1 / EPI2: ffn width
   const int* offsets;  // [E+1] row segments
-  const int* tile_off; // [E+1] tile prefix (row-grouped)
+  const int* tile_off; // [E+1] m-tile prefix (row-grouped, computed with this kernel's BM)
   int E;
   int M, N, K;         // k-grouped: M, N fixed; row-grouped: N, K fixed
-  int mtiles;          // k-grouped: tiles along M
 };
 
-constexpr int GBM = 128, GBN = 128, GBK = 64, GPITCH = GBK + 8;
+constexpr int GBM = 256, GBN = 256, GBK = 32, GSTAGES = 4;
+constexpr int GWM = 128, GWN = 64;         // 8 waves: 2 (m) x 4 (n), 128x64 each
+constexpr int GNT = 512;
+constexpr int GOPB = GBM * GBK * 2;       // bytes of one operand tile per stage (16 KB)
+constexpr int GSTAGE_B = 2 * GOPB;        // A + B per stage
+constexpr int GCP = GBN + 8;              // epilogue C tile pitch (elements)
+constexpr int GSMEM = (GSTAGES * GSTAGE_B > GBM * GCP * 2) ? GSTAGES * GSTAGE_B : GBM * GCP * 2;
+constexpr int GDMA = 4;                   // LDS-DMA instructions per wave per stage (2 per operand)
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// 16 zero bytes: the source of every DMA lane whose element lies past the reduction length.
+__device__ __attribute__((aligned(16))) const uint16_t g_zero16[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
 
+// s_waitcnt vmcnt(n) (expcnt / lgkmcnt left unconstrained), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS tile layouts (per operand, per stage), both fed by LDS-DMA (lane l of a wave
+// instruction writes bytes [16l, 16l+16) of a 1 KB block):
+//   rows tile  [256 i][32 k]: row i is 64 bytes = 4 chunks of 8 k; chunk c sits in slot
+//              c ^ ((i >> 2) & 3)  -> 16-byte fragment reads are bank-conflict free.
+//   cols tile  [32 k][256 i]: row k is 512 bytes = 32 chunks of 8 i; chunk c sits in slot
+//              c ^ ((k & 3) << 2)  -> the four k-rows a transposing read touches fall in
+//              four disjoint 64-byte bank groups.
+__device__ __forceinline__ int rows_off(int i, int c) { return i * 64 + ((c ^ ((i >> 2) & 3)) << 4); }
+__device__ __forceinline__ int cols_off(int k, int i) { return k * 512 + (((i >> 3) ^ ((k & 3) << 2)) << 4) + ((i & 7) << 1); }
+
+// Fragment (8 bf16) of a 32x32x16 MFMA operand: element j of lane l is (i = base + l%32, k = ks*16 + (l/32)*8 + j).
+__device__ __forceinline__ i16x8 frag_rows(const uint8_t* t, int base, int ks, int lane) {
+  const int i = base + (lane & 31);
+  return *reinterpret_cast<const i16x8*>(t + rows_off(i, ks * 2 + (lane >> 5)));
+}
+// Same fragment from a cols tile with two ds_read_b64_tr_b16: lane s of each 16-lane group
+// addresses (k0 + s/4, i0 + 4*(s%4)) and receives k0..k0+3 of column i0 + s.
+__device__ __forceinline__ i16x8 frag_cols(const uint8_t* t, int base, int ks, int lane) {
+  const int s = lane & 15;
+  const int i = base + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  const int k = ks * 16 + (lane >> 5) * 8 + (s >> 2);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(t + cols_off(k, i)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(t + cols_off(k + 4, i)));
+  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 template <int AMODE, int BMODE, int GROUP, int EPI>
-__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][GBM * GPITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][GBN * GPITCH];
+__global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
+  constexpr int NW_N = GBN / GWN;
+  constexpr int MI = GWM / 32, NI = GWN / 32;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GSMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
-  const int wm = wv >> 1;
-  const int wn = wv & 1;
+  const int wm0 = (wv / NW_N) * GWM;
+  const int wn0 = (wv % NW_N) * GWN;
 
-  // ---- tile decode ----
-  int e, mbase, mlen, kbase, klen;
-  const int n0 = blockIdx.y * GBN;
+  // ---- tile decode: XCD-contiguous logical order over a 1-D grid ----
+  const int P = gridDim.x;  // a multiple of 8
+  const int L = (int)(blockIdx.x & 7) * (P >> 3) + (int)(blockIdx.x >> 3);
+  int e, mbase, mlen, kbase, klen, nt;
   if constexpr (GROUP == 0) {
-    const int tile = blockIdx.x;
-    const int total = g.tile_off[g.E];
-    if (tile >= total) return;
-    int lo = 0, hi = g.E - 1;  // largest e with tile_off[e] <= tile
+    const int Tn = (EPI == 1) ? (2 * g.F + GBN - 1) / GBN : (g.N + GBN - 1) / GBN;
+    const int total = g.tile_off[g.E] * Tn;
+    if (L >= total) return;
+    int lo = 0, hi = g.E - 1;  // largest e with tile_off[e] * Tn <= L
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (g.tile_off[mid] <= tile) lo = mid;
+      if (g.tile_off[mid] * Tn <= L) lo = mid;
       else hi = mid - 1;
     }
     e = lo;
-    const int seg0 = g.offsets[e];
-    mbase = seg0 + (tile - g.tile_off[e]) * GBM;
+    const int cnt = g.tile_off[e + 1] - g.tile_off[e];
+    const int local = L - g.tile_off[e] * Tn;
+    nt = local / cnt;
+    const int mt = local - nt * cnt;
+    mbase = g.offsets[e] + mt * GBM;
     mlen = min(GBM, g.offsets[e + 1] - mbase);
     kbase = 0;
     klen = g.K;
   } else {
-    e = blockIdx.x / g.mtiles;
-    mbase = (blockIdx.x % g.mtiles) * GBM;
+    const int Tm = (g.M + GBM - 1) / GBM, Tn = (g.N + GBN - 1) / GBN;
+    if (L >= g.E * Tm * Tn) return;
+    e = L / (Tm * Tn);
+    const int r = L - e * Tm * Tn;
+    const int mt = r / Tn;
+    nt = r - mt * Tn;
+    mbase = mt * GBM;
     mlen = min(GBM, g.M - mbase);
     kbase = g.offsets[e];
     klen = g.offsets[e + 1] - kbase;
   }
-  const int nlen = (EPI == 1) ? min(GBN, 2 * (g.F - blockIdx.y * (GBN / 2))) : min(GBN, g.N - n0);
-
-  // ---- global -> register staging ----
-  u32x4 ra[4], rb[4];
-  const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
-
-  auto b_row_ptr = [&](int c, int k) -> const uint16_t* {
-    // B element (tile column c, absolute k) for BMODE 0 (rows)
-    if constexpr (EPI == 1) {
-      const int f = blockIdx.y * (GBN / 2) + (c >> 6) * 32 + (c & 31);
-      const uint16_t* base = ((c >> 5) & 1) ? g.B2 : g.B;
-      return base + (int64_t)e * g.b_estride + (int64_t)f * g.ldb + k;
-    } else {
-      return g.B + (int64_t)e * g.b_estride + (int64_t)(n0 + c) * g.ldb + k;
-    }
-  };
-
-  auto load_tile = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = tid + 256 * j;
-      if constexpr (AMODE == 0) {
-        const int r = q >> 3, kc = q & 7;
-        const int k = k0 + kc * 8;
-        const bool ok = r < mlen && k < klen;
-        ra[j] = ok ? *reinterpret_cast<const u32x4*>(g.A + (int64_t)(mbase + r) * g.lda + kbase + k) : zero4;
-      } else {
-        const int kk = q >> 4, mc = q & 15;
-        const int m = mbase + mc * 8;
-        const bool ok = (k0 + kk) < klen && m < g.M;
-        ra[j] = ok ? *reinterpret_cast<const u32x4*>(g.A + (int64_t)(kbase + k0 + kk) * g.lda + m) : zero4;
-      }
-      if constexpr (BMODE == 0) {
-        const int c = q >> 3, kc = q & 7;
-        const int k = k0 + kc * 8;
-        const bool ok = c < nlen && k < klen;
-        rb[j] = ok ? *reinterpret_cast<const u32x4*>(b_row_ptr(c, kbase + k)) : zero4;
-      } else {
-        const int kk = q >> 4, nc = q & 15;
-        const int n = n0 + nc * 8;
-        const int k = k0 + kk;
-        const bool ok = k < klen && n < g.N;
-        if (ok) {
-          const uint16_t* p;
-          if constexpr (GROUP == 0) {
-            const bool second = g.b_split > 0 && k >= g.b_split;
-            const int kr = second ? k - g.b_split : k;
-            p = (second ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)kr * g.ldb + n;
-          } else {
-            p = g.B + (int64_t)(kbase + k) * g.ldb + n;
-          }
-          rb[j] = *reinterpret_cast<const u32x4*>(p);
-        } else {
-          rb[j] = zero4;
-        }
-      }
-    }
-  };
-
-  auto store_tile = [&](int buf) {
-    uint16_t* as = As[buf];
-    uint16_t* bs = Bs[buf];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = tid + 256 * j;
-      if constexpr (AMODE == 0) {
-        *reinterpret_cast<u32x4*>(&as[(q >> 3) * GPITCH + (q & 7) * 8]) = ra[j];
-      } else {
-        const int kk = q >> 4, mc = q & 15;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          as[(mc * 8 + 2 * i) * GPITCH + kk] = (uint16_t)(ra[j][i] & 0xffffu);
-          as[(mc * 8 + 2 * i + 1) * GPITCH + kk] = (uint16_t)(ra[j][i] >> 16);
-        }
-      }
-      if constexpr (BMODE == 0) {
-        *reinterpret_cast<u32x4*>(&bs[(q >> 3) * GPITCH + (q & 7) * 8]) = rb[j];
-      } else {
-        const int kk = q >> 4, nc = q & 15;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          bs[(nc * 8 + 2 * i) * GPITCH + kk] = (uint16_t)(rb[j][i] & 0xffffu);
-          bs[(nc * 8 + 2 * i + 1) * GPITCH + kk] = (uint16_t)(rb[j][i] >> 16);
-        }
-      }
-    }
-  };
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[mi][ni][j] = 0.f;
-
+  const int n0 = nt * GBN;
+  const int nlen = (EPI == 1) ? min(GBN, 2 * (g.F - nt * (GBN / 2))) : min(GBN, g.N - n0);
   const int nk = (klen + GBK - 1) / GBK;
-  if (nk > 0) {
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int buf = kt & 1;
-      if (kt + 1 < nk) load_tile((kt + 1) * GBK);
-      const uint16_t* as = As[buf];
-      const uint16_t* bs = Bs[buf];
+
+  // ---- per-lane DMA sources.  Wave instruction j (= 2*wv + q, q = 0, 1) of an operand fills bytes
+  // [1024 j, 1024 j + 1024) of its stage tile: rows mode -> rows 16j + l/4, slot l%4;
+  // cols mode -> k-rows 2j + l/32, slot l%32. ----
+  const uint16_t* a_row[2];
+  const uint16_t* b_row[2];
+  int a_c[2], b_c[2], a_kr[2], b_kr[2], a_i[2], b_i[2];
 #pragma unroll
-      for (int ks = 0; ks < GBK / 16; ++ks) {
-        i16x8 fa[2], fb[2];
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-          fa[mi] = *reinterpret_cast<const i16x8*>(
-              &as[(wm * 64 + mi * 32 + (lane & 31)) * GPITCH + ks * 16 + (lane >> 5) * 8]);
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          fb[ni] = *reinterpret_cast<const i16x8*>(
-              &bs[(wn * 64 + ni * 32 + (lane & 31)) * GPITCH + ks * 16 + (lane >> 5) * 8]);
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-          for (int ni = 0; ni < 2; ++ni)
-            acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, fa[mi]), __builtin_bit_cast(bf16x8, fb[ni]),
-                                       acc[mi][ni]);
+  for (int q = 0; q < 2; ++q) {
+    const int j = 2 * wv + q;
+    if constexpr (AMODE == 0) {
+      const int i = 16 * j + (lane >> 2);
+      a_c[q] = (lane & 3) ^ ((i >> 2) & 3);
+      a_row[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase;
+    } else {
+      a_kr[q] = 2 * j + (lane >> 5);
+      a_i[q] = (((lane & 31) ^ ((a_kr[q] & 3) << 2)) << 3);
+    }
+    if constexpr (BMODE == 0) {
+      const int i = 16 * j + (lane >> 2);
+      b_c[q] = (lane & 3) ^ ((i >> 2) & 3);
+      const int ic = min(i, nlen - 1);
+      if constexpr (EPI == 1) {
+        const int f = nt * (GBN / 2) + (ic >> 6) * 32 + (ic & 31);
+        b_row[q] = (((ic >> 5) & 1) ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)f * g.ldb;
+      } else {
+        b_row[q] = g.B + (int64_t)e * g.b_estride + (int64_t)(n0 + ic) * g.ldb;
       }
-      if (kt + 1 < nk) store_tile(buf ^ 1);
-      __syncthreads();
+    } else {
+      b_kr[q] = 2 * j + (lane >> 5);
+      b_i[q] = (((lane & 31) ^ ((b_kr[q] & 3) << 2)) << 3);
     }
   }
 
-  // ---- epilogue: acc[mi][ni][j] = C[wm*64 + mi*32 + (j/4)*8 + (lane/32)*4 + j%4][wn*64 + ni*32 + lane%32] ----
+  auto issue = [&](int kt) {
+    const int k0 = min(kt, nk - 1) * GBK;
+    uint8_t* st = smem + (kt % GSTAGES) * GSTAGE_B;
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = wm * 64 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
-      if (r >= mlen) continue;
-      if constexpr (EPI == 1) {
-        const int f = blockIdx.y * (GBN / 2) + wn * 32 + (lane & 31);
-        if (f < g.F) {
-          const float gv = acc[mi][0][j];
-          const float uv = acc[mi][1][j];
-          const int64_t row = mbase + r;
-          g.C[row * g.ldc + f] = f2bf(silu_f(gv) * uv);
-          g.C2[row * 2 * (int64_t)g.F + f] = f2bf(gv);
-          g.C2[row * 2 * (int64_t)g.F + g.F + f] = f2bf(uv);
-        }
+    for (int q = 0; q < 2; ++q) {
+      const int j = 2 * wv + q;
+      const uint16_t* src;
+      if constexpr (AMODE == 0) {
+        const int k = k0 + a_c[q] * 8;
+        src = k < klen ? a_row[q] + k : g_zero16;
       } else {
+        const int k = k0 + a_kr[q];
+        const int i = mbase + a_i[q];
+        src = (k < klen && i < g.M) ? g.A + (int64_t)(kbase + k) * g.lda + i : g_zero16;
+      }
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(st + j * 1024), 16, 0, 0);
+    }
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          const int c = n0 + wn * 64 + ni * 32 + (lane & 31);
-          if (c >= g.N) continue;
-          const float v = acc[mi][ni][j];
-          if constexpr (EPI == 2) {
-            const int64_t row = mbase + r;
-            const float gv = bf2f(g.X[row * 2 * (int64_t)g.F + c]);
-            const float uv = bf2f(g.X[row * 2 * (int64_t)g.F + g.F + c]);
-            const float sg = 1.f / (1.f + __expf(-gv));
-            const float sl = gv * sg;
-            const float dsl = sg * (1.f + gv * (1.f - sg));
-            g.C[row * g.ldc + c] = f2bf(v * uv * dsl);
-            g.C[row * g.ldc + g.F + c] = f2bf(v * sl);
-          } else if constexpr (GROUP == 0) {
-            g.C[(int64_t)(mbase + r) * g.ldc + c] = f2bf(v);
-          } else {
-            const int m = mbase + r;
-            const bool second = g.c_split > 0 && m >= g.c_split;
-            uint16_t* base = (second ? g.C2 : g.C) + (int64_t)e * g.c_estride;
-            base[(int64_t)(second ? m - g.c_split : m) * g.ldc + c] = f2bf(v);
-          }
+    for (int q = 0; q < 2; ++q) {
+      const int j = 2 * wv + q;
+      const uint16_t* src;
+      if constexpr (BMODE == 0) {
+        const int k = k0 + b_c[q] * 8;
+        src = k < klen ? b_row[q] + k : g_zero16;
+      } else {
+        const int k = k0 + b_kr[q];
+        const int i = n0 + b_i[q];
+        const bool ok = k < klen && i < g.N;
+        if constexpr (GROUP == 0) {
+          const bool second = g.b_split > 0 && k >= g.b_split;
+          const int kr = second ? k - g.b_split : k;
+          src = ok ? (second ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)kr * g.ldb + i : g_zero16;
+        } else {
+          src = ok ? g.B + (int64_t)(kbase + k) * g.ldb + i : g_zero16;
         }
+      }
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(st + GOPB + j * 1024), 16, 0, 0);
+    }
+  };
+
+  f32x16 acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[mi][ni][j] = 0.f;
+
+  if (nk > 0) {
+#pragma unroll
+    for (int s = 0; s < GSTAGES - 1; ++s) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+      wait_vmcnt<(GSTAGES - 2) * GDMA>();  // this wave's part of stage kt has landed
+      __builtin_amdgcn_s_barrier();        // every wave's part has landed; stage kt-1 is consumed
+      issue(kt + GSTAGES - 1);             // refills the slot of stage kt-1 (clamped past the end)
+      const uint8_t* as = smem + (kt % GSTAGES) * GSTAGE_B;
+      const uint8_t* bs = as + GOPB;
+      // all fragments of the stage first (one LDS latency per stage), then the MFMAs
+      i16x8 fa[GBK / 16][MI], fb[GBK / 16][NI];
+#pragma unroll
+      for (int ks = 0; ks < GBK / 16; ++ks) {
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+          fa[ks][mi] = AMODE == 0 ? frag_rows(as, wm0 + mi * 32, ks, lane) : frag_cols(as, wm0 + mi * 32, ks, lane);
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+          fb[ks][ni] = BMODE == 0 ? frag_rows(bs, wn0 + ni * 32, ks, lane) : frag_cols(bs, wn0 + ni * 32, ks, lane);
+      }
+#pragma unroll
+      for (int ks = 0; ks < GBK / 16; ++ks)
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, fa[ks][mi]), __builtin_bit_cast(bf16x8, fb[ks][ni]),
+                                       acc[mi][ni]);
+    }
+    wait_vmcnt<0>();  // the clamped refills past the end land before the epilogue reuses the ring
+  }
+  __syncthreads();
+
+  // ---- epilogue: the bf16 C tile goes through LDS so every global access is a 16-byte row chunk.
+  // acc[mi][ni][j] = C[wm0 + mi*32 + (j/4)*8 + (lane/32)*4 + j%4][wn0 + ni*32 + lane%32]
+  constexpr int CP = GCP;
+  uint16_t* cs = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+        cs[r * CP + wn0 + ni * 32 + (lane & 31)] = f2bf(acc[mi][ni][j]);
+      }
+  __syncthreads();
+  const int BN = GBN, BM = GBM, NT = GNT;
+  if constexpr (EPI == 1) {
+    // tile column c: pair c/64, gate (c/32 even) or up (odd), f = nt*BN/2 + (c/64)*32 + c%32
+    constexpr int UPR = BN / 16;  // gate chunks of 8 per row
+    for (int u = tid; u < BM * UPR; u += NT) {
+      const int r = u / UPR, q = u % UPR;
+      const int cc = (q >> 2) * 64 + (q & 3) * 8;  // gate column of this chunk
+      const int f = nt * (BN / 2) + (q >> 2) * 32 + (q & 3) * 8;
+      if (r >= mlen || f >= g.F) continue;
+      const u32x4 gv = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc]);
+      const u32x4 uv = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc + 32]);
+      u32x4 av;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float g0 = __uint_as_float(gv[d] << 16), g1 = __uint_as_float(gv[d] & 0xffff0000u);
+        const float u0 = __uint_as_float(uv[d] << 16), u1 = __uint_as_float(uv[d] & 0xffff0000u);
+        av[d] = pack2bf(silu_f(g0) * u0, silu_f(g1) * u1);
+      }
+      const int64_t row = mbase + r;
+      *reinterpret_cast<u32x4*>(g.C + row * g.ldc + f) = av;
+      *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + f) = gv;
+      *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + g.F + f) = uv;
+    }
+  } else {
+    constexpr int UPR = BN / 8;
+    for (int u = tid; u < BM * UPR; u += NT) {
+      const int r = u / UPR, cc = (u % UPR) * 8;
+      const int c = n0 + cc;
+      if (r >= mlen || c >= g.N) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc]);
+      if constexpr (EPI == 2) {
+        const int64_t row = mbase + r;
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(g.X + row * 2 * (int64_t)g.F + c);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(g.X + row * 2 * (int64_t)g.F + g.F + c);
+        u32x4 dg, du;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          float da[2] = {__uint_as_float(v[d] << 16), __uint_as_float(v[d] & 0xffff0000u)};
+          float gg[2] = {__uint_as_float(gv[d] << 16), __uint_as_float(gv[d] & 0xffff0000u)};
+          float uu[2] = {__uint_as_float(uv[d] << 16), __uint_as_float(uv[d] & 0xffff0000u)};
+          float o1[2], o2[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float sg = 1.f / (1.f + __expf(-gg[h]));
+            const float sl = gg[h] * sg;
+            o1[h] = da[h] * uu[h] * sg * (1.f + gg[h] * (1.f - sg));
+            o2[h] = da[h] * sl;
+          }
+          dg[d] = pack2bf(o1[0], o1[1]);
+          du[d] = pack2bf(o2[0], o2[1]);
+        }
+        *reinterpret_cast<u32x4*>(g.C + row * g.ldc + c) = dg;
+        *reinterpret_cast<u32x4*>(g.C + row * g.ldc + g.F + c) = du;
+      } else if constexpr (GROUP == 0) {
+        *reinterpret_cast<u32x4*>(g.C + (int64_t)(mbase + r) * g.ldc + c) = v;
+      } else {
+        const int m = mbase + r;
+        const bool second = g.c_split > 0 && m >= g.c_split;
+        uint16_t* base = (second ? g.C2 : g.C) + (int64_t)e * g.c_estride;
+        *reinterpret_cast<u32x4*>(base + (int64_t)(second ? m - g.c_split : m) * g.ldc + c) = v;
       }
     }
   }
 }
 
-// tile_off[0] = 0, tile_off[e+1] = sum_{e' <= e} ceil(rows_e' / GBM)  (one block, E <= 1024).
-__global__ __launch_bounds__(1024) void k_gemm_tiles(const int* __restrict__ offsets, int E, int* __restrict__ tile_off) {
+// tile_off[0] = 0, tile_off[e+1] = sum_{e' <= e} ceil(rows_e' / bm)  (one block, E <= 1024).
+__global__ __launch_bounds__(1024) void k_gemm_tiles(const int* __restrict__ offsets, int E, int bm,
+                                                     int* __restrict__ tile_off) {
   __shared__ int part[1024];
   const int tid = threadIdx.x;
-  const int c = tid < E ? (offsets[tid + 1] - offsets[tid] + GBM - 1) / GBM : 0;
+  const int c = tid < E ? (offsets[tid + 1] - offsets[tid] + bm - 1) / bm : 0;
   part[tid] = c;
   __syncthreads();
   for (int o = 1; o < 1024; o <<= 1) {
@@ -293,12 +376,23 @@ __global__ __launch_bounds__(1024) void k_gemm_tiles(const int* __restrict__ off
 
 namespace {
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+unsigned round8(int64_t v) { return (unsigned)((v + 7) / 8 * 8); }
 
-template <int AM, int BM_, int GR, int EP>
-int launch(const char* name, dim3 grid, hipStream_t s, const GemmArgs& a) {
-  MOE_LAUNCH(name, (k_gemm<AM, BM_, GR, EP>), grid, dim3(256), 0, s, a);
+template <int AM, int BMD, int GR, int EP>
+int launch(const char* name, hipStream_t s, const GemmArgs& a, int64_t R) {
+  int64_t blocks;
+  if constexpr (GR == 0) {
+    const int64_t Tn = EP == 1 ? (2 * (int64_t)a.F + GBN - 1) / GBN : ((int64_t)a.N + GBN - 1) / GBN;
+    blocks = ((R + GBM - 1) / GBM + a.E) * Tn;
+  } else {
+    blocks = (int64_t)a.E * ((a.M + GBM - 1) / GBM) * ((a.N + GBN - 1) / GBN);
+  }
+  if (blocks <= 0) return 0;
+  MOE_LAUNCH(name, (k_gemm<AM, BMD, GR, EP>), dim3(round8(blocks)), dim3(GNT), 0, s, a);
   return check_launch(name);
 }
+
+constexpr int kTileBM = GBM;  // the row-grouped tile prefix is computed with the kernel's BM
 }  // namespace
 }  // namespace moe
 
@@ -319,8 +413,7 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   if (ws_bytes < moe_swiglu_workspace(E) || !workspace) return set_error("moe_swiglu_fwd: workspace"), MOE_EWORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int* tile_off = static_cast<int*>(workspace);
-  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, tile_off);
-  const unsigned mt = (unsigned)((R + GBM - 1) / GBM + E);
+  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off);
   GemmArgs a{};
   a.offsets = offsets;
   a.tile_off = tile_off;
@@ -338,7 +431,7 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   a.ldc = F;
   a.N = (int)(2 * F);
   a.K = (int)H;
-  if (int rc = launch<0, 0, 0, 1>("k_gemm_swiglu_fwd1", dim3(mt, (unsigned)((F + 63) / 64)), s, a)) return rc;
+  if (int rc = launch<0, 0, 0, 1>("k_gemm_swiglu_fwd1", s, a, R)) return rc;
   // fwd2: y = act . Wd^T
   GemmArgs b{};
   b.offsets = offsets;
@@ -354,7 +447,7 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   b.ldc = H;
   b.N = (int)H;
   b.K = (int)F;
-  return launch<0, 0, 0, 0>("k_gemm_swiglu_fwd2", dim3(mt, (unsigned)((H + GBN - 1) / GBN)), s, b);
+  return launch<0, 0, 0, 0>("k_gemm_swiglu_fwd2", s, b, R);
 }
 
 extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* hgu, const void* w_gate,
@@ -370,10 +463,9 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
   if (ws_bytes < moe_swiglu_workspace(E) || !workspace) return set_error("moe_swiglu_bwd: workspace"), MOE_EWORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int* tile_off = static_cast<int*>(workspace);
-  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, tile_off);
-  const unsigned mt = (unsigned)((std::max<int64_t>(R, 1) + GBM - 1) / GBM + E);
+  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off);
   // dA: dh = epilogue(dy . Wd)   (B[n=f][k=h] = Wd[h][f])
-  {
+  if (R > 0) {
     GemmArgs a{};
     a.offsets = offsets;
     a.tile_off = tile_off;
@@ -389,11 +481,10 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.X = static_cast<const uint16_t*>(hgu);
     a.N = (int)F;
     a.K = (int)H;
-    if (R > 0)
-      if (int rc = launch<0, 1, 0, 2>("k_gemm_swiglu_dact", dim3(mt, (unsigned)((F + GBN - 1) / GBN)), s, a)) return rc;
+    if (int rc = launch<0, 1, 0, 2>("k_gemm_swiglu_dact", s, a, R)) return rc;
   }
   // dxp = dh . [Wg ; Wu]   (B[n=h][k=j] = W1[j][h])
-  {
+  if (R > 0) {
     GemmArgs a{};
     a.offsets = offsets;
     a.tile_off = tile_off;
@@ -410,8 +501,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.ldc = H;
     a.N = (int)H;
     a.K = (int)(2 * F);
-    if (R > 0)
-      if (int rc = launch<0, 1, 0, 0>("k_gemm_swiglu_dxp", dim3(mt, (unsigned)((H + GBN - 1) / GBN)), s, a)) return rc;
+    if (int rc = launch<0, 1, 0, 0>("k_gemm_swiglu_dxp", s, a, R)) return rc;
   }
   // dWd_e = dy_e^T . act_e   (M = H, N = F, K = rows of e)
   {
@@ -427,10 +517,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.c_estride = H * F;
     a.M = (int)H;
     a.N = (int)F;
-    a.mtiles = (int)((H + GBM - 1) / GBM);
-    if (int rc = launch<1, 1, 1, 0>("k_gemm_swiglu_dwd", dim3((unsigned)(E * a.mtiles), (unsigned)((F + GBN - 1) / GBN)),
-                                    s, a))
-      return rc;
+    if (int rc = launch<1, 1, 1, 0>("k_gemm_swiglu_dwd", s, a, R)) return rc;
   }
   // [dWg_e ; dWu_e] = dh_e^T . xp_e   (M = 2F, N = H, K = rows of e)
   {
@@ -448,8 +535,6 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.c_estride = F * H;
     a.M = (int)(2 * F);
     a.N = (int)H;
-    a.mtiles = (int)((2 * F + GBM - 1) / GBM);
-    return launch<1, 1, 1, 0>("k_gemm_swiglu_dw1", dim3((unsigned)(E * a.mtiles), (unsigned)((H + GBN - 1) / GBN)),
-                              s, a);
+    return launch<1, 1, 1, 0>("k_gemm_swiglu_dw1", s, a, R);
   }
 }
