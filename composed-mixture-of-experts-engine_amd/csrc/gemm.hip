@@ -3,9 +3,10 @@
 // One kernel template covers the six products of the expert FFN forward and
 // backward.  Each computes C[m, n] = sum_k A[m, k] B[n, k] on
 // v_mfma_f32_32x32x16_bf16 with 256x256 block tiles (8 waves of 128x64) and
-// a 4-stage LDS ring of 32-wide k slices filled by LDS-DMA
-// (global_load_lds_dwordx4) three stages ahead, so no operand passes through
-// VGPRs and each load has three compute slices to land.  Blocks are numbered
+// a 4-stage LDS ring (128 KB) of 32-wide k slices filled by LDS-DMA
+// (global_load_lds_dwordx4) about three stages ahead, so no operand passes
+// through VGPRs and each load has three compute slices to land.  The LDS reads
+// of each 16-wide k half overlap the MFMAs of the previous half.  Blocks are numbered
 // so that each XCD (blockIdx mod 8) runs a contiguous range of logical tiles:
 // tiles that share a weight panel stay in one L2.
 //
@@ -73,6 +74,7 @@ constexpr int GDMA = 4;                   // LDS-DMA instructions per wave per s
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_void_t*)p; }
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // 16 zero bytes: the source of every DMA lane whose element lies past the reduction length.
@@ -85,6 +87,45 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+
+// One LDS-DMA instruction: lane l copies 16 bytes from src into LDS bytes [lds + 16 l, lds + 16 l + 16).
+// Issued from asm on purpose: the compiler tracks the builtin's LDS write and then makes every
+// LDS read it cannot disambiguate (the transposing reads below) wait for all DMA in flight
+// (vmcnt(0)), which would drain the ring each stage.  Completion is ordered by the explicit
+// vmcnt waits of the main loop instead.  (m0 is written by SALU and read by the DMA: one wait state.)
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
+  __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds) : "memory");
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Workgroup barrier without the vmcnt(0) drain __syncthreads implies (LDS-DMA stays in flight);
+// the empty asm statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+// Scheduling pattern for the machine scheduler: NM slots of one MFMA each.  The ND LDS reads of the
+// next k half are spread over the first NR slots (early, so their latency hides behind the later
+// MFMAs) and the NV LDS-DMA refills take one slot each at the end.
+template <int I, int NM, int NR, int ND, int NV>
+struct Interleave {
+  static __device__ __forceinline__ void run() {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    if constexpr (I < NR) {
+      constexpr int nd = ND * (I + 1) / NR - ND * I / NR;
+      if constexpr (nd > 0) __builtin_amdgcn_sched_group_barrier(0x100, nd, 0);  // DS read
+    }
+    if constexpr (I >= NM - NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    if constexpr (I + 1 < NM) Interleave<I + 1, NM, NR, ND, NV>::run();
+  }
+};
 
 // LDS tile layouts (per operand, per stage), both fed by LDS-DMA (lane l of a wave
 // instruction writes bytes [16l, 16l+16) of a 1 KB block):
@@ -120,7 +161,7 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS-DMA targets stay scalar
   const int wm0 = (wv / NW_N) * GWM;
   const int wn0 = (wv % NW_N) * GWN;
 
@@ -165,74 +206,69 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
 
   // ---- per-lane DMA sources.  Wave instruction j (= 2*wv + q, q = 0, 1) of an operand fills bytes
   // [1024 j, 1024 j + 1024) of its stage tile: rows mode -> rows 16j + l/4, slot l%4;
-  // cols mode -> k-rows 2j + l/32, slot l%32. ----
-  const uint16_t* a_row[2];
-  const uint16_t* b_row[2];
-  int a_c[2], b_c[2], a_kr[2], b_kr[2], a_i[2], b_i[2];
+  // cols mode -> k-rows 2j + l/32, slot l%32.  Only the k offset of a stage varies in the loop:
+  // rows mode adds k0 elements, cols mode k0 * ld (a wave-uniform product). ----
+  const uint16_t* a_src[2];
+  const uint16_t* b_src[2];
+  const uint16_t* b_src2[2];
+  int a_kl[2], b_kl[2];  // the lane's first k within a stage
+  bool a_ok[2], b_ok[2]; // the lane's row / column lies inside the tile
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int j = 2 * wv + q;
     if constexpr (AMODE == 0) {
       const int i = 16 * j + (lane >> 2);
-      a_c[q] = (lane & 3) ^ ((i >> 2) & 3);
-      a_row[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase;
+      a_kl[q] = ((lane & 3) ^ ((i >> 2) & 3)) * 8;
+      a_ok[q] = true;  // rows past the segment re-read its last row; their results are not stored
+      a_src[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase + a_kl[q];
     } else {
-      a_kr[q] = 2 * j + (lane >> 5);
-      a_i[q] = (((lane & 31) ^ ((a_kr[q] & 3) << 2)) << 3);
+      a_kl[q] = 2 * j + (lane >> 5);
+      const int i = (((lane & 31) ^ ((a_kl[q] & 3) << 2)) << 3);
+      a_ok[q] = i < mlen;
+      a_src[q] = g.A + (int64_t)(kbase + a_kl[q]) * g.lda + mbase + i;
     }
+    b_src2[q] = nullptr;
     if constexpr (BMODE == 0) {
       const int i = 16 * j + (lane >> 2);
-      b_c[q] = (lane & 3) ^ ((i >> 2) & 3);
+      b_kl[q] = ((lane & 3) ^ ((i >> 2) & 3)) * 8;
+      b_ok[q] = true;
       const int ic = min(i, nlen - 1);
       if constexpr (EPI == 1) {
         const int f = nt * (GBN / 2) + (ic >> 6) * 32 + (ic & 31);
-        b_row[q] = (((ic >> 5) & 1) ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)f * g.ldb;
+        b_src[q] = (((ic >> 5) & 1) ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)f * g.ldb + b_kl[q];
       } else {
-        b_row[q] = g.B + (int64_t)e * g.b_estride + (int64_t)(n0 + ic) * g.ldb;
+        b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)(n0 + ic) * g.ldb + b_kl[q];
       }
     } else {
-      b_kr[q] = 2 * j + (lane >> 5);
-      b_i[q] = (((lane & 31) ^ ((b_kr[q] & 3) << 2)) << 3);
+      b_kl[q] = 2 * j + (lane >> 5);
+      const int i = (((lane & 31) ^ ((b_kl[q] & 3) << 2)) << 3);
+      b_ok[q] = i < nlen;
+      if constexpr (GROUP == 0) {
+        b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)b_kl[q] * g.ldb + n0 + i;
+        if (g.b_split > 0) b_src2[q] = g.B2 + (int64_t)e * g.b_estride + (int64_t)b_kl[q] * g.ldb + n0 + i;
+      } else {
+        b_src[q] = g.B + (int64_t)(kbase + b_kl[q]) * g.ldb + n0 + i;
+      }
     }
   }
 
-  auto issue = [&](int kt) {
+  auto issue = [&](int kt, uint8_t* st) {
     const int k0 = min(kt, nk - 1) * GBK;
-    uint8_t* st = smem + (kt % GSTAGES) * GSTAGE_B;
+    const int64_t a_step = AMODE == 0 ? (int64_t)k0 : (int64_t)k0 * g.lda;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int j = 2 * wv + q;
-      const uint16_t* src;
-      if constexpr (AMODE == 0) {
-        const int k = k0 + a_c[q] * 8;
-        src = k < klen ? a_row[q] + k : g_zero16;
-      } else {
-        const int k = k0 + a_kr[q];
-        const int i = mbase + a_i[q];
-        src = (k < klen && i < g.M) ? g.A + (int64_t)(kbase + k) * g.lda + i : g_zero16;
-      }
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(st + j * 1024), 16, 0, 0);
+      const uint16_t* src = (a_ok[q] && k0 + a_kl[q] < klen) ? a_src[q] + a_step : g_zero16;
+      lds_dma16(src, lds_addr(st + (2 * wv + q) * 1024));
     }
+    // cols-mode B of the row-grouped products may switch source at k = b_split (a multiple of GBK,
+    // so a stage lies wholly on one side)
+    const bool second = BMODE == 1 && GROUP == 0 && g.b_split > 0 && k0 >= g.b_split;
+    const int kb = second ? k0 - g.b_split : k0;
+    const int64_t b_step = BMODE == 0 ? (int64_t)kb : (int64_t)kb * g.ldb;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int j = 2 * wv + q;
-      const uint16_t* src;
-      if constexpr (BMODE == 0) {
-        const int k = k0 + b_c[q] * 8;
-        src = k < klen ? b_row[q] + k : g_zero16;
-      } else {
-        const int k = k0 + b_kr[q];
-        const int i = n0 + b_i[q];
-        const bool ok = k < klen && i < g.N;
-        if constexpr (GROUP == 0) {
-          const bool second = g.b_split > 0 && k >= g.b_split;
-          const int kr = second ? k - g.b_split : k;
-          src = ok ? (second ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)kr * g.ldb + i : g_zero16;
-        } else {
-          src = ok ? g.B + (int64_t)(kbase + k) * g.ldb + i : g_zero16;
-        }
-      }
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(st + GOPB + j * 1024), 16, 0, 0);
+      const uint16_t* src = (b_ok[q] && k0 + b_kl[q] < klen) ? (second ? b_src2[q] : b_src[q]) + b_step : g_zero16;
+      lds_dma16(src, lds_addr(st + GOPB + (2 * wv + q) * 1024));
     }
   };
 
@@ -244,36 +280,53 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[mi][ni][j] = 0.f;
 
+  // Fragments of one 16-wide k half of a stage, and the MFMAs that consume them.
+  auto frags = [&](const uint8_t* as, int ks, i16x8 (&fa)[MI], i16x8 (&fb)[NI]) {
+    const uint8_t* bs = as + GOPB;
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+      fa[mi] = AMODE == 0 ? frag_rows(as, wm0 + mi * 32, ks, lane) : frag_cols(as, wm0 + mi * 32, ks, lane);
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+      fb[ni] = BMODE == 0 ? frag_rows(bs, wn0 + ni * 32, ks, lane) : frag_cols(bs, wn0 + ni * 32, ks, lane);
+  };
+  auto mma = [&](const i16x8 (&fa)[MI], const i16x8 (&fb)[NI]) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, fa[mi]), __builtin_bit_cast(bf16x8, fb[ni]), acc[mi][ni]);
+  };
+
+  // Software pipeline: the LDS reads of the next k half overlap the MFMAs of the current one.
+  // Iteration kt holds the first half of stage kt in registers on entry; the ring slot of stage kt
+  // is refilled with stage kt + GSTAGES once every wave has read its second half.
   if (nk > 0) {
 #pragma unroll
-    for (int s = 0; s < GSTAGES - 1; ++s) issue(s);
+    for (int s = 0; s < GSTAGES; ++s) issue(s, smem + s * GSTAGE_B);
+    i16x8 fa0[MI], fb0[NI], fa1[MI], fb1[NI];
+    wait_vmcnt<(GSTAGES - 1) * GDMA>();  // this wave's part of stage 0 has landed
+    lds_barrier();                       // every wave's part has
+    frags(smem, 0, fa0, fb0);
+    constexpr int NDS = (AMODE ? 2 : 1) * MI + (BMODE ? 2 : 1) * NI;  // LDS read instructions per k half
+    int slot = 0;
     for (int kt = 0; kt < nk; ++kt) {
-      wait_vmcnt<(GSTAGES - 2) * GDMA>();  // this wave's part of stage kt has landed
-      __builtin_amdgcn_s_barrier();        // every wave's part has landed; stage kt-1 is consumed
-      issue(kt + GSTAGES - 1);             // refills the slot of stage kt-1 (clamped past the end)
-      const uint8_t* as = smem + (kt % GSTAGES) * GSTAGE_B;
-      const uint8_t* bs = as + GOPB;
-      // all fragments of the stage first (one LDS latency per stage), then the MFMAs
-      i16x8 fa[GBK / 16][MI], fb[GBK / 16][NI];
-#pragma unroll
-      for (int ks = 0; ks < GBK / 16; ++ks) {
-#pragma unroll
-        for (int mi = 0; mi < MI; ++mi)
-          fa[ks][mi] = AMODE == 0 ? frag_rows(as, wm0 + mi * 32, ks, lane) : frag_cols(as, wm0 + mi * 32, ks, lane);
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-          fb[ks][ni] = BMODE == 0 ? frag_rows(bs, wn0 + ni * 32, ks, lane) : frag_cols(bs, wn0 + ni * 32, ks, lane);
-      }
-#pragma unroll
-      for (int ks = 0; ks < GBK / 16; ++ks)
-#pragma unroll
-        for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-          for (int ni = 0; ni < NI; ++ni)
-            acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, fa[ks][mi]), __builtin_bit_cast(bf16x8, fb[ks][ni]),
-                                       acc[mi][ni]);
+      uint8_t* const cur = smem + slot * GSTAGE_B;  // ring slot of stage kt
+      slot = slot + 1 == GSTAGES ? 0 : slot + 1;
+      frags(cur, 1, fa1, fb1);
+      mma(fa0, fb0);
+      Interleave<0, MI * NI, 4, NDS, 0>::run();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt_lgkm0<(GSTAGES - 2) * GDMA>();  // stage kt+1 landed; this wave's reads of slot kt are done
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(kt + GSTAGES, cur);                  // clamped past the end: re-reads the last stage, never read back
+      frags(smem + slot * GSTAGE_B, 0, fa0, fb0);
+      mma(fa1, fb1);
+      Interleave<0, MI * NI, 4, NDS, GDMA>::run();
+      __builtin_amdgcn_sched_barrier(0);
     }
-    wait_vmcnt<0>();  // the clamped refills past the end land before the epilogue reuses the ring
+    wait_vmcnt<0>();  // the clamped refills land before the epilogue reuses the ring
   }
   __syncthreads();
 
