@@ -47,6 +47,43 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_counters.md")
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of ``kernel`` on ``workload`` from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain
+    copy of known size), or None when the summary has no entry for it."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            text = f.read()
+    except OSError:
+        return None
+    start = text.find("```json")
+    if start < 0:
+        return None
+    end = text.find("```", start + 7)
+    try:
+        data = json.loads(text[start + 7:end])
+    except ValueError:
+        return None
+    ent = data.get("workloads", {}).get(workload, {}).get(kernel)
+    if ent is None:
+        return None
+    return int(ent["fetch_bytes"] + ent["write_bytes"])
+
+
+def copy_probe(torch):
+    """One plain 1 GiB device-to-device copy (torch copy kernel): the known-size reference that the
+    FETCH_SIZE / WRITE_SIZE counters are scaled by."""
+    src = torch.ones(1 << 29, dtype=torch.int16, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def timed(torch, step, steps, warmup):
     """Run warmup + timed steps with library per-kernel timing on; returns (ms/step, {kernel: (n, ms)})."""
     from moe_mi355 import _lib
@@ -120,7 +157,7 @@ def run_router(args, torch):
         "fwd_bwd_GBps": round(gbs, 1), "fwd_bwd_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
         "alg_bytes_per_step": alg["step"],
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, cfg.name),
                      "alg_bytes_per_launch": alg[dom], "avg_us": kernels[dom]["avg_us"]},
         "kernels": kernels,
     }
@@ -217,7 +254,8 @@ def run_layer(args, torch, cfg, layout, inp):
         "gemm_ms_per_step": round(gemm_ms, 4),
         "gemm_TFLOPs": round(step_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else None,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(dom, f"{cfg.name}:{layout}"),
                      "flops_per_launch": fl[dom], "avg_us": kernels[dom]["avg_us"]},
         "kernels": kernels,
     }
@@ -290,6 +328,8 @@ def main():
     ap.add_argument("--workload", default="layer", choices=["layer", "router", "dispatch", "skewed", "all"])
     ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run one 1 GiB device copy first (the size reference for HBM counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the expert-parallel "
@@ -304,6 +344,8 @@ def main():
     from moe_mi355 import configs
 
     log(f"[bench] workload={args.workload} steps={args.steps} warmup={args.warmup}")
+    if args.copy_probe:
+        copy_probe(torch)
     extra = {}
     if args.workload in ("layer", "all"):
         log("[bench] generating C4 inputs")
