@@ -18,9 +18,11 @@ timing starts; ``moe_mi355/configs.py``):
 
 One step = one forward + backward (forward only for dispatch).  W untimed
 warmup steps, then exactly K steps bracketed by torch.cuda.synchronize();
-prints ONE JSON line on stdout.  Per-kernel durations come from hipEvents
-that libmoe_mi355.so records around each of its launches during the timed
-region (same stream as the kernels).  The CPU baseline is the float64 oracle
+prints ONE JSON line on stdout.  Per-kernel durations come from a separate
+pass (after the timed one) in which libmoe_mi355.so records hipEvents around
+each of its launches on the launch stream.  The router leg is also replayed
+as a captured HIP graph (``graph_*`` fields: the rate without host launch
+overhead).  The CPU baseline is the float64 oracle
 timed on a bounded sample of the same workload on this host's cores.
 """
 
@@ -84,24 +86,56 @@ def copy_probe(torch):
     torch.cuda.empty_cache()
 
 
-def timed(torch, step, steps, warmup):
-    """Run warmup + timed steps with library per-kernel timing on; returns (ms/step, {kernel: (n, ms)})."""
+def timed(torch, step, steps, warmup, prof_steps=None):
+    """Run W warmup steps, then K timed steps bracketed by synchronize (no per-kernel events: ms/step is the
+    plain steady-state rate), then a separate pass of ``prof_steps`` steps with the library's per-launch
+    hipEvents on for the per-kernel table.  Returns (ms/step, {kernel: (launches, total ms)})."""
     from moe_mi355 import _lib
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    _lib.prof_enable(True)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0.record()
     for _ in range(steps):
         step()
     t1.record()
     torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    _lib.prof_enable(True)
+    for _ in range(prof_steps or steps):
+        step()
+    torch.cuda.synchronize()
     _lib.prof_enable(False)
-    return t0.elapsed_time(t1) / steps, _lib.prof_summary()
+    return ms, _lib.prof_summary()
+
+
+def graph_timed(torch, step, steps, warmup):
+    """The same step captured once as a HIP graph (torch.cuda.graph) and replayed K times: the rate without
+    host launch overhead.  Returns ms/step."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(max(warmup, 3)):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    del g
+    return t0.elapsed_time(t1) / steps
 
 
 def kernel_table(prof, work, unit_scale, unit):
@@ -146,6 +180,7 @@ def run_router(args, torch):
         torch.autograd.grad(out[1], (x, w), grad_outputs=gw)
 
     ms, prof = timed(torch, step, max(args.steps, 20), args.warmup)
+    gms = graph_timed(torch, step, max(args.steps, 20), args.warmup)
     alg = router_bytes(N, H, E, K)
     kernels = kernel_table(prof, alg, 1e9, "GBps")
     dom = max((k for k in kernels if k in alg), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
@@ -155,6 +190,8 @@ def run_router(args, torch):
         "workload": "C2 router fwd+bwd", "tokens": N, "d_model": H, "experts": E, "top_k": K,
         "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
         "fwd_bwd_GBps": round(gbs, 1), "fwd_bwd_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "graph_ms_per_step": gms, "graph_fwd_bwd_GBps": round(alg["step"] / (gms * 1e-3) / 1e9, 1),
+        "graph_fwd_bwd_frac_of_hbm_peak": round(alg["step"] / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "alg_bytes_per_step": alg["step"],
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, cfg.name),
@@ -235,14 +272,14 @@ def run_layer(args, torch, cfg, layout, inp):
             torch.autograd.grad(out, params, grad_outputs=gout)
 
     log(f"[bench] timing {cfg.name}")
-    ms, prof = timed(torch, step, args.steps, args.warmup)
+    ms, prof = timed(torch, step, args.steps, args.warmup, prof_steps=min(args.steps, 5))
     R = int(layer.last_plan.offsets[-1].item())  # rows run through the experts
     fl = gemm_flops(R, cfg.H, cfg.F)
     kernels = kernel_table(prof, fl, 1e12, "TFLOPs")
     dom = max((k for k in kernels if k in fl), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     achieved = kernels[dom]["TFLOPs"]
     step_flops = 18 * R * cfg.H * cfg.F
-    gemm_ms = sum(prof[k][1] for k in GEMM_KERNELS if k in prof) / args.steps
+    gemm_ms = sum(prof[k][1] / prof[k][0] for k in GEMM_KERNELS if k in prof)
     res = {
         "workload": f"{cfg.name} layer fwd+bwd ({layout} layout)", "tokens": cfg.T, "d_model": cfg.H,
         "experts": cfg.E, "ffn": cfg.F, "top_k": cfg.K, "rows_computed": R,

@@ -27,12 +27,9 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// float -> bf16, round to nearest even, NaN stays NaN: gfx950's v_cvt_pk_bf16_f32 (bit-identical to the
+// integer rounding u + 0x7fff + ((u >> 16) & 1) on every non-NaN input; checked exhaustively on the GPU).
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float load_f(const void* p, int dt, int64_t i) {
   return dt == MOE_BF16 ? bf2f(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
@@ -45,9 +42,11 @@ __device__ __forceinline__ void store_f(void* p, int dt, int64_t i, float v) {
     static_cast<float*>(p)[i] = v;
 }
 
-// Pack two floats as two bf16 in one dword (low half = a).
+// Pack two floats as two bf16 in one dword (low half = a), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack2bf(float a, float b) {
-  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
@@ -56,6 +55,17 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, 
 
 __device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations (lgkmcnt(0)) but, unlike
+// __syncthreads (whose fence also waits for every outstanding global load and store, vmcnt(0)), leaves global
+// prefetches and stores in flight.  The empty asm statements keep the compiler from moving memory accesses
+// across it.
+__device__ __forceinline__ void lds_sync() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4));  // vmcnt, expcnt unconstrained; lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
 }
 
 template <typename T>

@@ -63,13 +63,13 @@ struct GemmArgs {
 };
 
 constexpr int GBM = 256, GBN = 256, GBK = 32, GSTAGES = 4;
-constexpr int GWM = 128, GWN = 64;         // 8 waves: 2 (m) x 4 (n), 128x64 each
-constexpr int GNT = 512;
+// Wave layouts (template parameter NW): 8 waves of 128x64 (2 x 4, two waves per SIMD) or 4 waves of
+// 128x128 (2 x 2, one wave per SIMD with up to 512 registers: a third fewer LDS bytes per MFMA).
+constexpr int GWM = 128;
 constexpr int GOPB = GBM * GBK * 2;       // bytes of one operand tile per stage (16 KB)
 constexpr int GSTAGE_B = 2 * GOPB;        // A + B per stage
 constexpr int GCP = GBN + 8;              // epilogue C tile pitch (elements)
 constexpr int GSMEM = (GSTAGES * GSTAGE_B > GBM * GCP * 2) ? GSTAGES * GSTAGE_B : GBM * GCP * 2;
-constexpr int GDMA = 4;                   // LDS-DMA instructions per wave per stage (2 per operand)
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
@@ -153,8 +153,12 @@ __device__ __forceinline__ i16x8 frag_cols(const uint8_t* t, int base, int ks, i
   return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-template <int AMODE, int BMODE, int GROUP, int EPI>
-__global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
+template <int AMODE, int BMODE, int GROUP, int EPI, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
+  constexpr int GNT = NW * 64;
+  constexpr int GWN = NW == 8 ? 64 : 128;
+  constexpr int QPW = (GOPB / 1024) / NW;  // LDS-DMA instructions per wave per operand per stage
+  constexpr int GDMA = 2 * QPW;            // ... for both operands
   constexpr int NW_N = GBN / GWN;
   constexpr int MI = GWM / 32, NI = GWN / 32;
   __shared__ __attribute__((aligned(16))) uint8_t smem[GSMEM];
@@ -204,18 +208,18 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
   const int nlen = (EPI == 1) ? min(GBN, 2 * (g.F - nt * (GBN / 2))) : min(GBN, g.N - n0);
   const int nk = (klen + GBK - 1) / GBK;
 
-  // ---- per-lane DMA sources.  Wave instruction j (= 2*wv + q, q = 0, 1) of an operand fills bytes
+  // ---- per-lane DMA sources.  Wave instruction j (= QPW*wv + q, q < QPW) of an operand fills bytes
   // [1024 j, 1024 j + 1024) of its stage tile: rows mode -> rows 16j + l/4, slot l%4;
   // cols mode -> k-rows 2j + l/32, slot l%32.  Only the k offset of a stage varies in the loop:
   // rows mode adds k0 elements, cols mode k0 * ld (a wave-uniform product). ----
-  const uint16_t* a_src[2];
-  const uint16_t* b_src[2];
-  const uint16_t* b_src2[2];
-  int a_kl[2], b_kl[2];  // the lane's first k within a stage
-  bool a_ok[2], b_ok[2]; // the lane's row / column lies inside the tile
+  const uint16_t* a_src[QPW];
+  const uint16_t* b_src[QPW];
+  const uint16_t* b_src2[QPW];
+  int a_kl[QPW], b_kl[QPW];  // the lane's first k within a stage
+  bool a_ok[QPW], b_ok[QPW]; // the lane's row / column lies inside the tile
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int j = 2 * wv + q;
+  for (int q = 0; q < QPW; ++q) {
+    const int j = QPW * wv + q;
     if constexpr (AMODE == 0) {
       const int i = 16 * j + (lane >> 2);
       a_kl[q] = ((lane & 3) ^ ((i >> 2) & 3)) * 8;
@@ -256,9 +260,9 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
     const int k0 = min(kt, nk - 1) * GBK;
     const int64_t a_step = AMODE == 0 ? (int64_t)k0 : (int64_t)k0 * g.lda;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < QPW; ++q) {
       const uint16_t* src = (a_ok[q] && k0 + a_kl[q] < klen) ? a_src[q] + a_step : g_zero16;
-      lds_dma16(src, lds_addr(st + (2 * wv + q) * 1024));
+      lds_dma16(src, lds_addr(st + (QPW * wv + q) * 1024));
     }
     // cols-mode B of the row-grouped products may switch source at k = b_split (a multiple of GBK,
     // so a stage lies wholly on one side)
@@ -266,9 +270,9 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
     const int kb = second ? k0 - g.b_split : k0;
     const int64_t b_step = BMODE == 0 ? (int64_t)kb : (int64_t)kb * g.ldb;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < QPW; ++q) {
       const uint16_t* src = (b_ok[q] && k0 + b_kl[q] < klen) ? (second ? b_src2[q] : b_src[q]) + b_step : g_zero16;
-      lds_dma16(src, lds_addr(st + GOPB + (2 * wv + q) * 1024));
+      lds_dma16(src, lds_addr(st + GOPB + (QPW * wv + q) * 1024));
     }
   };
 
@@ -315,7 +319,7 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
       slot = slot + 1 == GSTAGES ? 0 : slot + 1;
       frags(cur, 1, fa1, fb1);
       mma(fa0, fb0);
-      Interleave<0, MI * NI, 4, NDS, 0>::run();
+      Interleave<0, MI * NI, MI * NI / 2, NDS, 0>::run();
       __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt_lgkm0<(GSTAGES - 2) * GDMA>();  // stage kt+1 landed; this wave's reads of slot kt are done
       lds_barrier();
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(GNT, 1) void k_gemm(GemmArgs g) {
       issue(kt + GSTAGES, cur);                  // clamped past the end: re-reads the last stage, never read back
       frags(smem + slot * GSTAGE_B, 0, fa0, fb0);
       mma(fa1, fb1);
-      Interleave<0, MI * NI, 4, NDS, GDMA>::run();
+      Interleave<0, MI * NI, MI * NI / 2, NDS, GDMA>::run();
       __builtin_amdgcn_sched_barrier(0);
     }
     wait_vmcnt<0>();  // the clamped refills land before the epilogue reuses the ring
@@ -431,7 +435,7 @@ namespace {
 bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 unsigned round8(int64_t v) { return (unsigned)((v + 7) / 8 * 8); }
 
-template <int AM, int BMD, int GR, int EP>
+template <int AM, int BMD, int GR, int EP, int NW>
 int launch(const char* name, hipStream_t s, const GemmArgs& a, int64_t R) {
   int64_t blocks;
   if constexpr (GR == 0) {
@@ -441,11 +445,17 @@ int launch(const char* name, hipStream_t s, const GemmArgs& a, int64_t R) {
     blocks = (int64_t)a.E * ((a.M + GBM - 1) / GBM) * ((a.N + GBN - 1) / GBN);
   }
   if (blocks <= 0) return 0;
-  MOE_LAUNCH(name, (k_gemm<AM, BMD, GR, EP>), dim3(round8(blocks)), dim3(GNT), 0, s, a);
+  MOE_LAUNCH(name, (k_gemm<AM, BMD, GR, EP, NW>), dim3(round8(blocks)), dim3(NW * 64), 0, s, a);
   return check_launch(name);
 }
 
-constexpr int kTileBM = GBM;  // the row-grouped tile prefix is computed with the kernel's BM
+constexpr int kTileBM = GBM;
+// wave layout per product (8: 8 waves of 128x64, 4: 4 waves of 128x128)
+#ifndef MOE_GEMM_NW
+#define MOE_GEMM_NW 8
+#endif
+constexpr int kNW_fwd1 = MOE_GEMM_NW, kNW_fwd2 = MOE_GEMM_NW, kNW_dact = MOE_GEMM_NW, kNW_dxp = MOE_GEMM_NW,
+              kNW_dwd = MOE_GEMM_NW, kNW_dw1 = MOE_GEMM_NW;  // the row-grouped tile prefix is computed with the kernel's BM
 }  // namespace
 }  // namespace moe
 
@@ -484,7 +494,7 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   a.ldc = F;
   a.N = (int)(2 * F);
   a.K = (int)H;
-  if (int rc = launch<0, 0, 0, 1>("k_gemm_swiglu_fwd1", s, a, R)) return rc;
+  if (int rc = launch<0, 0, 0, 1, kNW_fwd1>("k_gemm_swiglu_fwd1", s, a, R)) return rc;
   // fwd2: y = act . Wd^T
   GemmArgs b{};
   b.offsets = offsets;
@@ -500,7 +510,7 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   b.ldc = H;
   b.N = (int)H;
   b.K = (int)F;
-  return launch<0, 0, 0, 0>("k_gemm_swiglu_fwd2", s, b, R);
+  return launch<0, 0, 0, 0, kNW_fwd2>("k_gemm_swiglu_fwd2", s, b, R);
 }
 
 extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* hgu, const void* w_gate,
@@ -534,7 +544,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.X = static_cast<const uint16_t*>(hgu);
     a.N = (int)F;
     a.K = (int)H;
-    if (int rc = launch<0, 1, 0, 2>("k_gemm_swiglu_dact", s, a, R)) return rc;
+    if (int rc = launch<0, 1, 0, 2, kNW_dact>("k_gemm_swiglu_dact", s, a, R)) return rc;
   }
   // dxp = dh . [Wg ; Wu]   (B[n=h][k=j] = W1[j][h])
   if (R > 0) {
@@ -554,7 +564,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.ldc = H;
     a.N = (int)H;
     a.K = (int)(2 * F);
-    if (int rc = launch<0, 1, 0, 0>("k_gemm_swiglu_dxp", s, a, R)) return rc;
+    if (int rc = launch<0, 1, 0, 0, kNW_dxp>("k_gemm_swiglu_dxp", s, a, R)) return rc;
   }
   // dWd_e = dy_e^T . act_e   (M = H, N = F, K = rows of e)
   {
@@ -570,7 +580,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.c_estride = H * F;
     a.M = (int)H;
     a.N = (int)F;
-    if (int rc = launch<1, 1, 1, 0>("k_gemm_swiglu_dwd", s, a, R)) return rc;
+    if (int rc = launch<1, 1, 1, 0, kNW_dwd>("k_gemm_swiglu_dwd", s, a, R)) return rc;
   }
   // [dWg_e ; dWu_e] = dh_e^T . xp_e   (M = 2F, N = H, K = rows of e)
   {
@@ -588,6 +598,6 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     a.c_estride = F * H;
     a.M = (int)(2 * F);
     a.N = (int)H;
-    return launch<1, 1, 1, 0>("k_gemm_swiglu_dw1", s, a, R);
+    return launch<1, 1, 1, 0, kNW_dw1>("k_gemm_swiglu_dw1", s, a, R);
   }
 }

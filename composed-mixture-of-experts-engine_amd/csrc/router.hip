@@ -532,6 +532,96 @@ __global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__
 // Writes G (f32) and, when gb != nullptr, G rounded to bf16 in a zero-padded
 // [N, ekp] layout.
 // ---------------------------------------------------------------------------
+// dL/dlogits of one token, LPT lanes per token, lane `sub` owning experts sub + LPT*j (j < EPL):
+//   softmax p, renormalised top-k weights v_k = p_{e_k} / max(sum_k p_{e_k}, 1e-30) with upstream gw,
+//   aux term ca * p (f - sum p f) with f_e = cnt_e / (N K), z term cz * lse * p.
+struct GCoef {
+  float ca, cz, inv_nk;
+};
+
+__device__ __forceinline__ GCoef glogit_coef(const float* __restrict__ grad_aux, const float* __restrict__ grad_z,
+                                             float aux_coef, float z_coef, int N, int E, int K) {
+  const float ga = grad_aux ? grad_aux[0] : 1.f;
+  const float gz = grad_z ? grad_z[0] : 1.f;
+  return GCoef{aux_coef * ga * (float)E / (float)N, z_coef * gz * 2.f / (float)N, 1.f / ((float)N * (float)K)};
+}
+
+template <int LPT, int EPL>
+__device__ __forceinline__ void glogit_token(const float* __restrict__ logits, const int64_t* __restrict__ idx,
+                                             const void* __restrict__ gw, int gw_dt,
+                                             const int64_t* __restrict__ cnt, const GCoef& c, int t, int E, int K,
+                                             int sub, float (&gl)[EPL]) {
+  float lg[EPL], p[EPL], f[EPL], gp[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = sub + LPT * j;
+    lg[j] = (e < E) ? logits[(int64_t)t * E + e] : -INFINITY;
+    f[j] = (e < E && c.ca != 0.f) ? (float)cnt[e] * c.inv_nk : 0.f;
+    gp[j] = 0.f;
+  }
+  float m = lg[0];
+#pragma unroll
+  for (int j = 1; j < EPL; ++j) m = fmaxf(m, lg[j]);
+#pragma unroll
+  for (int o = LPT / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    p[j] = expf(lg[j] - m);
+    s += p[j];
+  }
+#pragma unroll
+  for (int o = LPT / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  const float inv = 1.f / s;
+  const float lse = m + logf(s);
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) p[j] *= inv;
+  if (gw != nullptr) {
+    // S = max(sum v, 1e-30); gwv = sum gw*v; grad_v = gw/S - gwv/S^2
+    float S = 0.f, gwv = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int e = (int)idx[(int64_t)t * K + k];
+      const float v = expf(logits[(int64_t)t * E + e] - m) * inv;
+      const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
+      S += v;
+      gwv += gk * v;
+    }
+    S = fmaxf(S, 1e-30f);
+    const float iS = 1.f / S;
+    for (int k = 0; k < K; ++k) {
+      const int e = (int)idx[(int64_t)t * K + k];
+      const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
+      const float gv = gk * iS - gwv * iS * iS;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (e == sub + LPT * j) gp[j] += gv;
+    }
+  }
+  float inner = 0.f, pf = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    inner += gp[j] * p[j];
+    pf += p[j] * f[j];
+  }
+#pragma unroll
+  for (int o = LPT / 2; o > 0; o >>= 1) {
+    inner += __shfl_xor(inner, o);
+    pf += __shfl_xor(pf, o);
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    float v = p[j] * (gp[j] - inner);
+    if (c.ca != 0.f) v += c.ca * p[j] * (f[j] - pf);
+    if (c.cz != 0.f) v += c.cz * lse * p[j];
+    gl[j] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward 1: G = dL/dlogits.  LPT lanes per token (EPL experts per lane).
+// Writes G (f32) and, when gb != nullptr, G rounded to bf16 in a zero-padded
+// [N, ekp] layout.
+// ---------------------------------------------------------------------------
 template <int LPT, int EPL>
 __global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict__ logits,
                                                         const int64_t* __restrict__ idx, const void* __restrict__ gw,
@@ -545,84 +635,23 @@ __global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict_
   const int sub = lane % LPT;
   const int slot = lane / LPT;
   const int wpb = blockDim.x >> 6;
-  const float ga = grad_aux ? grad_aux[0] : 1.f;
-  const float gz = grad_z ? grad_z[0] : 1.f;
-  const float ca = aux_coef * ga * (float)E / (float)N;
-  const float cz = z_coef * gz * 2.f / (float)N;
-  const float inv_nk = 1.f / ((float)N * (float)K);
+  const GCoef c = glogit_coef(grad_aux, grad_z, aux_coef, z_coef, N, E, K);
   const int stride = gridDim.x * wpb * TPW;
   for (int tb = (blockIdx.x * wpb + (threadIdx.x >> 6)) * TPW; tb < N; tb += stride) {
     const int t_raw = tb + slot;
     const bool valid = t_raw < N;
     const int t = valid ? t_raw : N - 1;
-    float lg[EPL], p[EPL], f[EPL], gp[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const int e = sub + LPT * j;
-      lg[j] = (e < E) ? logits[(int64_t)t * E + e] : -INFINITY;
-      f[j] = (e < E && ca != 0.f) ? (float)cnt[e] * inv_nk : 0.f;
-      gp[j] = 0.f;
-    }
-    float m = lg[0];
-#pragma unroll
-    for (int j = 1; j < EPL; ++j) m = fmaxf(m, lg[j]);
-#pragma unroll
-    for (int o = LPT / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      p[j] = expf(lg[j] - m);
-      s += p[j];
-    }
-#pragma unroll
-    for (int o = LPT / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    const float inv = 1.f / s;
-    const float lse = m + logf(s);
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) p[j] *= inv;
-    if (gw != nullptr) {
-      // S = max(sum v, 1e-30); gwv = sum gw*v; grad_v = gw/S - gwv/S^2
-      float S = 0.f, gwv = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const int e = (int)idx[(int64_t)t * K + k];
-        const float v = expf(logits[(int64_t)t * E + e] - m) * inv;
-        const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
-        S += v;
-        gwv += gk * v;
-      }
-      S = fmaxf(S, 1e-30f);
-      const float iS = 1.f / S;
-      for (int k = 0; k < K; ++k) {
-        const int e = (int)idx[(int64_t)t * K + k];
-        const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
-        const float gv = gk * iS - gwv * iS * iS;
-#pragma unroll
-        for (int j = 0; j < EPL; ++j)
-          if (e == sub + LPT * j) gp[j] += gv;
-      }
-    }
-    float inner = 0.f, pf = 0.f;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      inner += gp[j] * p[j];
-      pf += p[j] * f[j];
-    }
-#pragma unroll
-    for (int o = LPT / 2; o > 0; o >>= 1) {
-      inner += __shfl_xor(inner, o);
-      pf += __shfl_xor(pf, o);
-    }
+    float gl[EPL];
+    glogit_token<LPT, EPL>(logits, idx, gw, gw_dt, cnt, c, t, E, K, sub, gl);
     if (valid) {
 #pragma unroll
       for (int j = 0; j < EPL; ++j) {
         const int e = sub + LPT * j;
         if (e < E) {
-          float gl = p[j] * (gp[j] - inner);
-          if (ca != 0.f) gl += ca * p[j] * (f[j] - pf);
-          if (cz != 0.f) gl += cz * lse * p[j];
-          if (round_bf16) gl = bf2f(f2bf(gl));
-          G[(int64_t)t * E + e] = gl;
-          if (gb) gb[(int64_t)t * ekp + e] = f2bf(gl);
+          float v = gl[j];
+          if (round_bf16) v = bf2f(f2bf(v));
+          G[(int64_t)t * E + e] = v;
+          if (gb) gb[(int64_t)t * ekp + e] = f2bf(v);
         }
       }
       if (gb) {
@@ -708,7 +737,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_bf16(const uint16_t* __rest
   if (tbeg < tend) load_x(tbeg);
 
   for (int ts0 = tbeg; ts0 < tend; ts0 += kBwdTS) {
-    __syncthreads();  // previous step done with xs / dxs / gs / gts
+    lds_sync();  // previous step done with xs / dxs / gs / gts (global prefetch and dx stores stay in flight)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int q = tid + 256 * j;
@@ -725,7 +754,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_bf16(const uint16_t* __rest
       if (e < NTE * 16) gts[e * GTP + r] = v;
     }
     if (ts0 + kBwdTS < tend) load_x(ts0 + kBwdTS);
-    __syncthreads();
+    lds_sync();
 
     if (wave_active) {
       // ---- dwg partial: D[m=h][n=e] += sum_t x[t][h] G[t][e] ----
@@ -761,7 +790,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_bf16(const uint16_t* __rest
         }
       }
     }
-    __syncthreads();
+    lds_sync();
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int q = tid + 256 * j;
@@ -787,6 +816,157 @@ __global__ __launch_bounds__(256) void k_router_dxdw_bf16(const uint16_t* __rest
           if (h < H && e < E) out[(int64_t)h * E + e] = accw[mt][ne][i];
         }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Backward 2, streaming form (bf16 x bf16, E <= 32, H % 256 == 0): dx = G wg^T and the dwg partial
+// x^T G of one (token chunk, 256 hidden columns) block.  Each wave owns 64 hidden columns and a private
+// LDS tile, so after the chunk's G has been staged (token-major and expert-major) the token loop has no
+// workgroup barrier: per 32-token step the wave writes its x tile to LDS, reads the dwg A operand with
+// transposing reads, forms dx with MFMA into the same tile and stores it as 128-byte row segments.  x is
+// prefetched two steps ahead with clamped (branch-free) loads; rows past the chunk read as zero.
+// ---------------------------------------------------------------------------
+constexpr int kSTC = 256;   // max tokens per chunk (a multiple of 64)
+constexpr int kSXP = 72;    // pitch (bf16) of a wave's 32 x 64 tile: 144 bytes, conflict-free for the reads below
+typedef short sh4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) sh4 lds_sh4;
+
+template <int NTE>
+__global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ wg,
+                                                            const uint16_t* __restrict__ gb, int N, int H, int E,
+                                                            int tc_len, int nht, uint16_t* __restrict__ dx,
+                                                            float* __restrict__ ws_dw) {
+  constexpr int GP = 32 + 8;         // token-major G row pitch (32 expert slots)
+  constexpr int GTP = kSTC + 8;      // expert-major G row pitch
+  __shared__ __attribute__((aligned(16))) uint16_t gs[kSTC * GP];
+  __shared__ __attribute__((aligned(16))) uint16_t gts[NTE * 16 * GTP];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[4][32 * kSXP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int chunk = blockIdx.x / nht;
+  const int ht = blockIdx.x - chunk * nht;
+  const int tbeg = chunk * tc_len;
+  const int tend = min(N, tbeg + tc_len);
+  const int nst = ((tend - tbeg + 63) / 64) * 2;  // 32-token steps, rounded up to even
+  const int col0 = ht * 256 + wv * 64;            // this wave's first hidden column
+  uint16_t* xsw = xs[wv];
+
+  // x stream: lane loads rows (lane/8) + 8j of the step, 16-byte chunk lane%8 of the wave's 64 columns
+  // (rows past the chunk re-read its last row and are zeroed when written to LDS)
+  const uint16_t* xw = x + col0 + (lane & 7) * 8;
+  auto load_x = [&](u32x4(&r)[4], int ts0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = ts0 + (lane >> 3) + 8 * j;
+      r[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xw + (int64_t)min(t, tend - 1) * H));
+    }
+  };
+  u32x4 xa[4], xb[4];
+  load_x(xa, tbeg);
+  load_x(xb, tbeg + 32);
+
+  // ---- stage the chunk's G (bf16, [N, 32] zero-padded rows) in both layouts; rows past the chunk are 0 ----
+  for (int q = tid; q < nst * 32 * 4; q += 256) {  // 4 x 16 bytes per token row
+    const int r = q >> 2, c8 = (q & 3) * 8;
+    const int t = tbeg + r;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(gb + (int64_t)min(t, tend - 1) * 32 + c8);
+    const bool ok = t < tend;
+    const u32x4 w = u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
+    *reinterpret_cast<u32x4*>(&gs[r * GP + c8]) = w;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = c8 + j;
+      if (e < NTE * 16) gts[e * GTP + r] = (uint16_t)(w[j >> 1] >> ((j & 1) * 16));
+    }
+  }
+
+  // gate fragments for dx: B[k = e][n = h] = wg[h][e]
+  i16x8 wB[4];
+#pragma unroll
+  for (int nc = 0; nc < 4; ++nc) {
+    const int h = col0 + nc * 16 + n;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = g * 8 + j;
+      wB[nc][j] = (short)wg[(int64_t)h * E + min(e, E - 1)];
+      if (e >= E) wB[nc][j] = 0;
+    }
+  }
+  f32x4 accw[4][NTE];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ne = 0; ne < NTE; ++ne) accw[mt][ne] = f32x4{0.f, 0.f, 0.f, 0.f};
+  lds_sync();  // G staged
+
+  // One 32-token step.  The refill of r (two steps ahead) is issued as soon as the tile is in LDS and
+  // before this step's dx stores: loads and stores retire in order on one counter, so a refill issued
+  // after the stores could only be waited for together with them.
+  auto step = [&](u32x4(&r)[4], int s) {
+    const int lr0 = 32 * s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = tbeg + lr0 + (lane >> 3) + 8 * j < tend;
+      const u32x4 v = r[j];
+      *reinterpret_cast<u32x4*>(&xsw[((lane >> 3) + 8 * j) * kSXP + (lane & 7) * 8]) =
+          u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
+    }
+    load_x(r, tbeg + lr0 + 64);
+    // dwg: D[m = h][n = e] += sum_t x[t][h] G[t][e]; A from two transposing reads: x[8g .. 8g+7][mt*16 + n]
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int cc = mt * 16 + 4 * (n & 3);
+      const sh4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sh4*)&xsw[(8 * g + (n >> 2)) * kSXP + cc]);
+      const sh4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sh4*)&xsw[(8 * g + 4 + (n >> 2)) * kSXP + cc]);
+      const i16x8 a = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int ne = 0; ne < NTE; ++ne) {
+        const i16x8 b = *reinterpret_cast<const i16x8*>(&gts[(ne * 16 + n) * GTP + lr0 + g * 8]);
+        accw[mt][ne] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), accw[mt][ne]);
+      }
+    }
+    // dx: D[m = t][n = h] = sum_e G[t][e] wg[h][e], written over the x tile
+#pragma unroll
+    for (int mk = 0; mk < 2; ++mk) {
+      const i16x8 a = *reinterpret_cast<const i16x8*>(&gs[(lr0 + mk * 16 + n) * GP + g * 8]);
+#pragma unroll
+      for (int nc = 0; nc < 4; ++nc) {
+        const f32x4 d = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, wB[nc]),
+                                     f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xsw[(mk * 16 + g * 4 + i) * kSXP + nc * 16 + n] = f2bf(d[i]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int lr = (lane >> 3) + 8 * j;
+      const int t = tbeg + lr0 + lr;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&xsw[lr * kSXP + (lane & 7) * 8]);
+      if (t < tend) *reinterpret_cast<u32x4*>(dx + (int64_t)t * H + col0 + (lane & 7) * 8) = v;
+    }
+  };
+
+  for (int s = 0; s < nst; s += 2) {
+    step(xa, s);
+    step(xb, s + 1);
+  }
+
+  float* out = ws_dw + (int64_t)chunk * H * E;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ne = 0; ne < NTE; ++ne)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = col0 + mt * 16 + g * 4 + i;
+        const int e = ne * 16 + n;
+        if (e < E) out[(int64_t)h * E + e] = accw[mt][ne][i];
+      }
 }
 
 // Generic dx = G wg^T: one thread per (t, h).
@@ -904,6 +1084,7 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
 
 struct BwdPlan {
   bool mfma;
+  bool stream;  // k_router_dxdw_stream (E <= 32, H % 256 == 0)
   int EK, NTE;
   int nchunk, tc_len;
   size_t off_g, off_gb, off_ws, total;
@@ -917,7 +1098,14 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   p.NTE = (int)((E + 15) / 16);
   if (p.NTE == 3) p.NTE = 4;
   if (p.NTE > 4 && p.NTE < 8) p.NTE = 8;
-  if (p.mfma) {
+  p.stream = p.mfma && E <= 32 && H % 256 == 0;
+  if (p.stream) {
+    // ~768 blocks (three per CU); chunks of a multiple of 64 tokens, at most kSTC
+    const int nht = (int)(H / 256);
+    const int want = std::max(1, 768 / nht);
+    p.tc_len = std::min(kSTC, std::max(64, cdiv(cdiv(N, want), 64) * 64));
+    p.nchunk = cdiv(N, p.tc_len);
+  } else if (p.mfma) {
     const int nhb = cdiv(H, 256);
     int nchunk = std::max(1, 1024 / nhb);
     const int max_chunks = cdiv(N, kBwdTS);
@@ -960,6 +1148,14 @@ void launch_fwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const i16x8* w
   constexpr int U = fwd_u(NT);
   MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_bf16<NT, HS, U>), grid, dim3(256), 0, s, x, wp, bias, N, H, E, K, idx, w, w_dt,
                      logits, lse, pc, pp, pz);
+}
+
+template <int NTE>
+void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, const uint16_t* gb, int N, int H, int E,
+                        int tc_len, int nchunk, uint16_t* dx, float* ws) {
+  const int nht = H / 256;
+  MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)), dim3(256), 0, s, x, wg, gb,
+             N, H, E, tc_len, nht, dx, ws);
 }
 
 template <int EK, int NTE>
@@ -1094,7 +1290,14 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
   }
   if (int rc = check_launch("k_router_glogits")) return rc;
   int nchunk = p.nchunk;
-  if (mfma) {
+  if (mfma && p.stream) {
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const uint16_t* wb = static_cast<const uint16_t*>(wg);
+    uint16_t* dxb = static_cast<uint16_t*>(dx_out);
+    if (p.NTE == 1) launch_dxdw_stream<1>(s, xb, wb, gb, (int)N, (int)H, (int)E, p.tc_len, p.nchunk, dxb, wsdw);
+    else launch_dxdw_stream<2>(s, xb, wb, gb, (int)N, (int)H, (int)E, p.tc_len, p.nchunk, dxb, wsdw);
+    if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+  } else if (mfma) {
     const dim3 grid(p.nchunk, cdiv(H, 256));
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     const uint16_t* wb = static_cast<const uint16_t*>(wg);
