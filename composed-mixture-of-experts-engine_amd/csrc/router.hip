@@ -36,7 +36,9 @@ constexpr int kMaxE = 256;
 // Gate pack: wg [H, E] bf16 -> wp[c][nt][lane] (16 bytes each) with
 // element j of lane l = wg[c*32 + (l/16)*8 + j][nt*16 + l%16], zero padded.
 // ---------------------------------------------------------------------------
-__global__ void k_pack_gate(const uint16_t* __restrict__ wg, int H, int E, int NT, i16x8* __restrict__ wp) {
+__global__ void k_pack_gate(const uint16_t* __restrict__ wg, int H, int E, int NT, i16x8* __restrict__ wp,
+                            unsigned* __restrict__ ticket) {
+  if (ticket != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *ticket = 0u;
   const int64_t total = (int64_t)((H + 31) / 32) * NT * 64;
   for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (int64_t)gridDim.x * blockDim.x) {
     const int lane = (int)(q & 63);
@@ -54,6 +56,123 @@ __global__ void k_pack_gate(const uint16_t* __restrict__ wg, int H, int E, int N
       v[j] = (e < E && k < H) ? val : (short)0;
     }
     wp[q] = v;
+  }
+}
+
+// Routing epilogue of one 16-token group: acc[nt][i] = logits[t0 + g*4 + i][nt*16 + n] (16x16 MFMA
+// layout).  Adds the bias, writes logits / lse / top-k ids / renormalised weights, counts the picks in
+// s_cnt (LDS atomics) and leaves the group's probability sums, z sum and non-finite count in
+// s_p[0 .. NT*16), *s_z, *s_nf.
+template <int NT>
+__device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int lane, const float* __restrict__ bias,
+                                            int N, int E, int K, int64_t* __restrict__ idx_out,
+                                            void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
+                                            float* __restrict__ lse_out, int* s_cnt, float* s_p, float* s_z,
+                                            int* s_nf) {
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  float pacc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
+  float zacc = 0.f;
+  int nf = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tt = t0 + g * 4 + i;
+    const bool valid = tt < N;
+    float lg[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int e = nt * 16 + n;
+      float v = acc[nt][i];
+      if (bias != nullptr && e < E) v += bias[e];
+      if (valid && e < E) {
+        logits_out[(int64_t)tt * E + e] = v;
+        if (!isfinite(v)) ++nf;
+      }
+      if (v != v) v = -INFINITY;  // NaN never wins a top-k slot
+      lg[nt] = (e < E) ? v : -INFINITY;
+    }
+    float m = lg[0];
+#pragma unroll
+    for (int nt = 1; nt < NT; ++nt) m = fmaxf(m, lg[nt]);
+    m = row16_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) s += expf(lg[nt] - m);
+    s = row16_sum(s);
+    const float inv = 1.f / s;
+    const float lse = m + logf(s);
+    if (valid) {
+      if (n == 0) lse_out[tt] = lse;
+      zacc += lse * lse;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) pacc[nt] += expf(lg[nt] - m) * inv;
+    }
+
+    // top-k: K rounds of row argmax; round r's winner is kept by lane r % 16.
+    uint32_t sel = 0;
+    int e_slot0 = 0, e_slot1 = 0;
+    float p_slot0 = 0.f, p_slot1 = 0.f;
+    float psum = 0.f;
+    for (int r = 0; r < K; ++r) {
+      float bv = -INFINITY;
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int e = nt * 16 + n;
+        if (e < E && !((sel >> nt) & 1u) && better(lg[nt], e, bv, be)) {
+          bv = lg[nt];
+          be = e;
+        }
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oe = __shfl_xor(be, o);
+        if (better(ov, oe, bv, be)) {
+          bv = ov;
+          be = oe;
+        }
+      }
+      if ((be & 15) == n) sel |= 1u << (be >> 4);
+      const float pv = expf(bv - m) * inv;
+      psum += pv;
+      if (r == n) {
+        e_slot0 = be;
+        p_slot0 = pv;
+      } else if (r == n + 16) {
+        e_slot1 = be;
+        p_slot1 = pv;
+      }
+    }
+    const float rden = 1.f / fmaxf(psum, 1e-30f);
+    if (valid) {
+      if (n < K) {
+        idx_out[(int64_t)tt * K + n] = e_slot0;
+        store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0 * rden);
+        atomicAdd(&s_cnt[e_slot0], 1);
+      }
+      if (n + 16 < K) {
+        idx_out[(int64_t)tt * K + n + 16] = e_slot1;
+        store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1 * rden);
+        atomicAdd(&s_cnt[e_slot1], 1);
+      }
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float v = pacc[nt];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (g == 0) s_p[nt * 16 + n] = v;
+  }
+  zacc += __shfl_xor(zacc, 16);
+  zacc += __shfl_xor(zacc, 32);
+  nf = wave_sum(nf);
+  if (lane == 0) {
+    *s_z = zacc;
+    *s_nf = nf;
   }
 }
 
@@ -159,112 +278,8 @@ __global__ __launch_bounds__(256) void k_router_fwd_bf16(
     }
   }
 
-  if (hp == 0) {
-    // ---- epilogue: lane holds logits[t0 + g*4 + i][nt*16 + n], i = 0..3 ----
-    float pacc[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
-    float zacc = 0.f;
-    int nf = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tt = t0 + g * 4 + i;
-      const bool valid = tt < N;
-      float lg[NT];
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int e = nt * 16 + n;
-        float v = acc[nt][i];
-        if (bias != nullptr && e < E) v += bias[e];
-        if (valid && e < E) {
-          logits_out[(int64_t)tt * E + e] = v;
-          if (!isfinite(v)) ++nf;
-        }
-        if (v != v) v = -INFINITY;  // NaN never wins a top-k slot
-        lg[nt] = (e < E) ? v : -INFINITY;
-      }
-      float m = lg[0];
-#pragma unroll
-      for (int nt = 1; nt < NT; ++nt) m = fmaxf(m, lg[nt]);
-      m = row16_max(m);
-      float s = 0.f;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) s += expf(lg[nt] - m);
-      s = row16_sum(s);
-      const float inv = 1.f / s;
-      const float lse = m + logf(s);
-      if (valid) {
-        if (n == 0) lse_out[tt] = lse;
-        zacc += lse * lse;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) pacc[nt] += expf(lg[nt] - m) * inv;
-      }
-
-      // top-k: K rounds of row argmax; round r's winner is kept by lane r % 16.
-      uint32_t sel = 0;
-      int e_slot0 = 0, e_slot1 = 0;
-      float p_slot0 = 0.f, p_slot1 = 0.f;
-      float psum = 0.f;
-      for (int r = 0; r < K; ++r) {
-        float bv = -INFINITY;
-        int be = 0x7fffffff;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int e = nt * 16 + n;
-          if (e < E && !((sel >> nt) & 1u) && better(lg[nt], e, bv, be)) {
-            bv = lg[nt];
-            be = e;
-          }
-        }
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) {
-          const float ov = __shfl_xor(bv, o);
-          const int oe = __shfl_xor(be, o);
-          if (better(ov, oe, bv, be)) {
-            bv = ov;
-            be = oe;
-          }
-        }
-        if ((be & 15) == n) sel |= 1u << (be >> 4);
-        const float pv = expf(bv - m) * inv;
-        psum += pv;
-        if (r == n) {
-          e_slot0 = be;
-          p_slot0 = pv;
-        } else if (r == n + 16) {
-          e_slot1 = be;
-          p_slot1 = pv;
-        }
-      }
-      const float rden = 1.f / fmaxf(psum, 1e-30f);
-      if (valid) {
-        if (n < K) {
-          idx_out[(int64_t)tt * K + n] = e_slot0;
-          store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0 * rden);
-          atomicAdd(&s_cnt[e_slot0], 1);
-        }
-        if (n + 16 < K) {
-          idx_out[(int64_t)tt * K + n + 16] = e_slot1;
-          store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1 * rden);
-          atomicAdd(&s_cnt[e_slot1], 1);
-        }
-      }
-    }
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      float v = pacc[nt];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (g == 0) s_p[tg][nt * 16 + n] = v;
-    }
-    zacc += __shfl_xor(zacc, 16);
-    zacc += __shfl_xor(zacc, 32);
-    nf = wave_sum(nf);
-    if (lane == 0) {
-      s_z[tg] = zacc;
-      s_nf[tg] = nf;
-    }
-  }
+  if (hp == 0) route_group<NT>(acc, t0, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt, s_p[tg],
+                              &s_z[tg], &s_nf[tg]);
   __syncthreads();
   // ---- per-block partials (fixed-order sums over token groups) ----
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
@@ -285,6 +300,283 @@ __global__ __launch_bounds__(256) void k_router_fwd_bf16(
     part_z[2 * blockIdx.x] = z;
     part_z[2 * blockIdx.x + 1] = (float)nfs;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Finalize: fixed-order sums of the per-block partials -> cnt, stats, aux, z (one block of NTHR threads).
+// ---------------------------------------------------------------------------
+template <int NTHR>
+__device__ __forceinline__ void router_finalize_block(const int* __restrict__ part_cnt, const float* __restrict__ part_p,
+                                                      const float* __restrict__ part_z, int nblk, int N, int E, int K,
+                                                      float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
+                                                      float* __restrict__ stats, float* __restrict__ aux_out,
+                                                      float* __restrict__ z_out) {
+  __shared__ float s_c[kMaxE];
+  __shared__ float s_pe[kMaxE];
+  __shared__ float s_red[2][NTHR / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // threads per expert: a power of two <= 64 so each expert's threads sit in one wave
+  int tpe = 1;
+  while (tpe * 2 <= 64 && tpe * 2 * E <= NTHR) tpe *= 2;
+  const int epp = NTHR / tpe;  // experts per pass
+  for (int e0 = 0; e0 < E; e0 += epp) {
+    const int e = e0 + tid / tpe;
+    const int j = tid % tpe;
+    int c = 0;
+    float p = 0.f;
+    if (e < E) {
+      int b = j;
+      for (; b + 7 * tpe < nblk; b += 8 * tpe) {  // 8 independent loads in flight
+        int cv[8];
+        float pv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          cv[u] = part_cnt[(int64_t)(b + u * tpe) * E + e];
+          pv[u] = part_p[(int64_t)(b + u * tpe) * E + e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          c += cv[u];
+          p += pv[u];
+        }
+      }
+      for (; b < nblk; b += tpe) {
+        c += part_cnt[(int64_t)b * E + e];
+        p += part_p[(int64_t)b * E + e];
+      }
+    }
+    for (int o = tpe / 2; o > 0; o >>= 1) {
+      c += __shfl_xor(c, o);
+      p += __shfl_xor(p, o);
+    }
+    if (j == 0 && e < E) {
+      cnt_out[e] = c;
+      s_c[e] = (float)c;
+      s_pe[e] = p / (float)N;
+      stats[MOE_STATS_HEAD + e] = p / (float)N;
+    }
+  }
+  float z = 0.f, nf = 0.f;
+  {
+    int b = tid;
+    for (; b + 3 * NTHR < nblk; b += 4 * NTHR) {
+      f32x4 zz;
+      float nn[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        zz[u] = part_z[2 * (b + u * NTHR)];
+        nn[u] = part_z[2 * (b + u * NTHR) + 1];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        z += zz[u];
+        nf += nn[u];
+      }
+    }
+    for (; b < nblk; b += NTHR) {
+      z += part_z[2 * b];
+      nf += part_z[2 * b + 1];
+    }
+  }
+  z = wave_sum(z);
+  nf = wave_sum(nf);
+  if (lane == 0) {
+    s_red[0][tid >> 6] = z;
+    s_red[1][tid >> 6] = nf;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    z = s_red[0][0];
+    nf = s_red[1][0];
+    for (int w = 1; w < NTHR / 64; ++w) {
+      z += s_red[0][w];
+      nf += s_red[1][w];
+    }
+    double tot = 0.0, mx = 0.0, aux = 0.0;
+    for (int e = 0; e < E; ++e) {
+      tot += s_c[e];
+      mx = fmax(mx, (double)s_c[e]);
+      aux += ((double)s_c[e] / ((double)N * K)) * (double)s_pe[e];
+    }
+    const double mean = tot / E;
+    double var = 0.0;
+    for (int e = 0; e < E; ++e) var += ((double)s_c[e] - mean) * ((double)s_c[e] - mean);
+    const float zstat = z / (float)N;
+    const float aux_raw = (float)(aux * E);
+    stats[0] = zstat;
+    stats[1] = aux_raw;
+    stats[2] = mean < 1e-9 ? 1.f : (float)(mx / mean);
+    stats[3] = (float)mean;
+    stats[4] = E > 1 ? (float)sqrt(var / (E - 1)) : NAN;
+    stats[5] = (float)tot;
+    stats[6] = nf;
+    stats[7] = 0.f;
+    if (aux_out) aux_out[0] = aux_coef * aux_raw;
+    if (z_out) z_out[0] = z_coef * zstat;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__ part_cnt,
+                                                         const float* __restrict__ part_p,
+                                                         const float* __restrict__ part_z, int nblk, int N, int E,
+                                                         int K, float aux_coef, float z_coef,
+                                                         int64_t* __restrict__ cnt_out, float* __restrict__ stats,
+                                                         float* __restrict__ aux_out, float* __restrict__ z_out) {
+  router_finalize_block<256>(part_cnt, part_p, part_z, nblk, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out, z_out);
+}
+
+// ---------------------------------------------------------------------------
+// Forward, streaming form (bf16 x bf16, E <= 32, H % 256 == 0).  Block = 8 waves = TG groups of 16 tokens.
+// Wave w streams the 32-wide hidden chunks w, w + 8, w + 16, ... of all the block's tokens, so every
+// packed-gate fragment it loads serves TG token groups; U chunks per prefetch group, double-buffered and
+// branch-free.  The 8 partial logit tiles are summed in LDS in wave order, waves 0 .. TG-1 route one group
+// each, and the block's partial statistics go to part_*.  The last block to finish (ticket counter, reset
+// by k_pack_gate before the launch) folds all blocks' partials: the finalize needs no launch of its own.
+// ---------------------------------------------------------------------------
+template <int NT, int TG, int U>
+__global__ __launch_bounds__(512) void k_router_fwd_stream(
+    const uint16_t* __restrict__ x, const i16x8* __restrict__ wp, const float* __restrict__ bias, int N, int H,
+    int E, int K, int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
+    float* __restrict__ lse_out, int* __restrict__ part_cnt, float* __restrict__ part_p, float* __restrict__ part_z,
+    unsigned* __restrict__ ticket, float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
+    float* __restrict__ stats, float* __restrict__ aux_out, float* __restrict__ z_out) {
+  __shared__ f32x4 s_acc[8][TG][NT][64];
+  __shared__ int s_cnt[NT * 16];
+  __shared__ float s_p[TG][NT * 16];
+  __shared__ float s_z[TG];
+  __shared__ int s_nf[TG];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int t0 = blockIdx.x * (16 * TG);
+  for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
+
+  // lane (g, n) of group q loads row t0 + 16q + n (clamped), k = 32c + 8g .. +8 of chunk c: the A fragment
+  const i16x8* xr[TG];
+#pragma unroll
+  for (int q = 0; q < TG; ++q) {
+    const int row = min(t0 + 16 * q + n, N - 1);
+    xr[q] = reinterpret_cast<const i16x8*>(x + (int64_t)row * H) + g;
+  }
+  const i16x8* wb = wp + lane;
+  const int nci = H >> 8;  // chunks per wave
+
+  f32x4 acc[TG][NT];
+#pragma unroll
+  for (int q = 0; q < TG; ++q)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  i16x8 a0[U][TG], a1[U][TG], b0[U][NT], b1[U][NT];
+  auto load_grp = [&](i16x8(&a)[U][TG], i16x8(&b)[U][NT], int i) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = wv + 8 * (i + u);
+#pragma unroll
+      for (int q = 0; q < TG; ++q) a[u][q] = __builtin_nontemporal_load(xr[q] + c * 4);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[(c * NT + nt) * 64];
+    }
+  };
+  auto mma_grp = [&](const i16x8(&a)[U][TG], const i16x8(&b)[U][NT]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < TG; ++q)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[q][nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a[u][q]), __builtin_bit_cast(bf16x8, b[u][nt]),
+                                    acc[q][nt]);
+  };
+  // the scheduling barriers keep the order "issue the next group's loads, then the MFMAs of the current
+  // group": left free, the scheduler interleaves them and the waits then drain the prefetch
+  int i = 0;
+  const int npair = nci / (2 * U);
+  if (npair > 0) {
+    load_grp(a0, b0, 0);
+    for (int pr = 0; pr < npair - 1; ++pr) {
+      load_grp(a1, b1, i + U);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_grp(a0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_grp(a0, b0, i + 2 * U);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_grp(a1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      i += 2 * U;
+    }
+    load_grp(a1, b1, i + U);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_grp(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_grp(a1, b1);
+    i += 2 * U;
+  }
+  for (; i < nci; ++i) {
+    const int c = wv + 8 * i;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+      const i16x8 a = __builtin_nontemporal_load(xr[q] + c * 4);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[q][nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, wb[(c * NT + nt) * 64]),
+                                  acc[q][nt]);
+    }
+  }
+
+#pragma unroll
+  for (int q = 0; q < TG; ++q)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) s_acc[wv][q][nt][lane] = acc[q][nt];
+  __syncthreads();  // partial tiles visible, s_cnt zeroed
+  if (wv < TG) {
+    f32x4 lg[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      lg[nt] = s_acc[0][wv][nt][lane];
+#pragma unroll
+      for (int w = 1; w < 8; ++w) lg[nt] += s_acc[w][wv][nt][lane];
+    }
+    route_group<NT>(lg, t0 + 16 * wv, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt, s_p[wv],
+                    &s_z[wv], &s_nf[wv]);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 512) {
+    float p = 0.f;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) p += s_p[q][e];
+    part_cnt[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+    part_p[(int64_t)blockIdx.x * E + e] = p;
+  }
+  if (threadIdx.x == 0) {
+    float z = 0.f;
+    int nfs = 0;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+      z += s_z[q];
+      nfs += s_nf[q];
+    }
+    part_z[2 * blockIdx.x] = z;
+    part_z[2 * blockIdx.x + 1] = (float)nfs;
+  }
+  // ---- the last block folds every block's partials.  The barrier orders every thread's partial stores
+  // before thread 0's agent-scope release (cumulative), so one fence per block publishes them; the last
+  // block's acquire makes all blocks' partials visible to it. ----
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  router_finalize_block<512>(part_cnt, part_p, part_z, gridDim.x, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out,
+                             z_out);
+  if (threadIdx.x == 0) *ticket = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -413,117 +705,6 @@ __global__ __launch_bounds__(256) void k_route_from_logits(const float* __restri
   if (threadIdx.x == 0) {
     part_z[2 * blockIdx.x] = ((s_z[0] + s_z[1]) + s_z[2]) + s_z[3];
     part_z[2 * blockIdx.x + 1] = (float)(s_nf[0] + s_nf[1] + s_nf[2] + s_nf[3]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Finalize: fixed-order sums of the per-block partials -> cnt, stats.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__ part_cnt,
-                                                         const float* __restrict__ part_p,
-                                                         const float* __restrict__ part_z, int nblk, int N, int E,
-                                                         int K, float aux_coef, float z_coef,
-                                                         int64_t* __restrict__ cnt_out, float* __restrict__ stats,
-                                                         float* __restrict__ aux_out, float* __restrict__ z_out) {
-  __shared__ float s_c[kMaxE];
-  __shared__ float s_pe[kMaxE];
-  __shared__ float s_red[2][4];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  // threads per expert: a power of two <= 64 so each expert's threads sit in one wave
-  int tpe = 1;
-  while (tpe * 2 <= 64 && tpe * 2 * E <= 256) tpe *= 2;
-  const int epp = 256 / tpe;  // experts per pass
-  for (int e0 = 0; e0 < E; e0 += epp) {
-    const int e = e0 + tid / tpe;
-    const int j = tid % tpe;
-    int c = 0;
-    float p = 0.f;
-    if (e < E) {
-      int b = j;
-      for (; b + 7 * tpe < nblk; b += 8 * tpe) {  // 8 independent loads in flight
-        int cv[8];
-        float pv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          cv[u] = part_cnt[(int64_t)(b + u * tpe) * E + e];
-          pv[u] = part_p[(int64_t)(b + u * tpe) * E + e];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          c += cv[u];
-          p += pv[u];
-        }
-      }
-      for (; b < nblk; b += tpe) {
-        c += part_cnt[(int64_t)b * E + e];
-        p += part_p[(int64_t)b * E + e];
-      }
-    }
-    for (int o = tpe / 2; o > 0; o >>= 1) {
-      c += __shfl_xor(c, o);
-      p += __shfl_xor(p, o);
-    }
-    if (j == 0 && e < E) {
-      cnt_out[e] = c;
-      s_c[e] = (float)c;
-      s_pe[e] = p / (float)N;
-      stats[MOE_STATS_HEAD + e] = p / (float)N;
-    }
-  }
-  float z = 0.f, nf = 0.f;
-  {
-    int b = tid;
-    for (; b + 3 * 256 < nblk; b += 4 * 256) {
-      f32x4 zz;
-      float nn[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        zz[u] = part_z[2 * (b + u * 256)];
-        nn[u] = part_z[2 * (b + u * 256) + 1];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        z += zz[u];
-        nf += nn[u];
-      }
-    }
-    for (; b < nblk; b += 256) {
-      z += part_z[2 * b];
-      nf += part_z[2 * b + 1];
-    }
-  }
-  z = wave_sum(z);
-  nf = wave_sum(nf);
-  if (lane == 0) {
-    s_red[0][tid >> 6] = z;
-    s_red[1][tid >> 6] = nf;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    z = ((s_red[0][0] + s_red[0][1]) + s_red[0][2]) + s_red[0][3];
-    nf = ((s_red[1][0] + s_red[1][1]) + s_red[1][2]) + s_red[1][3];
-    double tot = 0.0, mx = 0.0, aux = 0.0;
-    for (int e = 0; e < E; ++e) {
-      tot += s_c[e];
-      mx = fmax(mx, (double)s_c[e]);
-      aux += ((double)s_c[e] / ((double)N * K)) * (double)s_pe[e];
-    }
-    const double mean = tot / E;
-    double var = 0.0;
-    for (int e = 0; e < E; ++e) var += ((double)s_c[e] - mean) * ((double)s_c[e] - mean);
-    const float zstat = z / (float)N;
-    const float aux_raw = (float)(aux * E);
-    stats[0] = zstat;
-    stats[1] = aux_raw;
-    stats[2] = mean < 1e-9 ? 1.f : (float)(mx / mean);
-    stats[3] = (float)mean;
-    stats[4] = E > 1 ? (float)sqrt(var / (E - 1)) : NAN;
-    stats[5] = (float)tot;
-    stats[6] = nf;
-    stats[7] = 0.f;
-    if (aux_out) aux_out[0] = aux_coef * aux_raw;
-    if (z_out) z_out[0] = z_coef * zstat;
   }
 }
 
@@ -1051,9 +1232,10 @@ int fwd_tokens_per_block(int NT) { return 16 * (4 / fwd_hs(NT)); }
 
 struct FwdPlan {
   bool mfma;
-  int NT;
+  bool stream;  // k_router_fwd_stream (E <= 32, H % 256 == 0)
+  int NT, TG;
   int nblk;
-  size_t off_wp, off_cnt, off_p, off_z, total;
+  size_t off_wp, off_cnt, off_p, off_z, off_ticket, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1064,7 +1246,12 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   p.NT = (int)((E + 15) / 16);
   if (p.NT == 3) p.NT = 4;
   if (p.NT > 4 && p.NT < 8) p.NT = 8;
-  if (p.mfma) {
+  p.stream = p.mfma && E <= 32 && H % 256 == 0;
+  if (p.stream) {
+    // 16 * TG tokens per block: the largest TG that still gives one block per CU (256)
+    p.TG = N >= 256 * 64 ? 4 : (N >= 256 * 32 ? 2 : 1);
+    p.nblk = cdiv(N, 16 * p.TG);
+  } else if (p.mfma) {
     p.nblk = cdiv(N, fwd_tokens_per_block(p.NT));
   } else {
     p.nblk = (int)std::min<int64_t>(512, std::max<int64_t>(1, (N + 15) / 16));
@@ -1078,6 +1265,8 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   off += align256((size_t)p.nblk * E * sizeof(float));
   p.off_z = off;
   off += align256((size_t)p.nblk * 2 * sizeof(float));
+  p.off_ticket = off;
+  off += 256;
   p.total = off;
   return p;
 }
@@ -1138,6 +1327,16 @@ void launch_reduce(hipStream_t s, const float* ws, int nchunk, int64_t len, void
     const unsigned nb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (len + 63) / 64));
     MOE_LAUNCH("k_reduce_chunks", k_reduce_chunks<1>, dim3(nb), dim3(256), 0, s, ws, nchunk, len, out, out_dt);
   }
+}
+
+template <int NT, int TG>
+void launch_fwd_stream(int nblk, hipStream_t s, const uint16_t* x, const i16x8* wp, const float* bias, int N, int H,
+                       int E, int K, int64_t* idx, void* w, int w_dt, float* logits, float* lse, int* pc, float* pp,
+                       float* pz, unsigned* ticket, float aux_coef, float z_coef, int64_t* cnt, float* stats,
+                       float* aux_out, float* z_out) {
+  constexpr int U = 4;
+  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_stream<NT, TG, U>), dim3(nblk), dim3(512), 0, s, x, wp, bias, N, H, E, K,
+             idx, w, w_dt, logits, lse, pc, pp, pz, ticket, aux_coef, z_coef, cnt, stats, aux_out, z_out);
 }
 
 template <int NT>
@@ -1202,10 +1401,28 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
   if (mfma) {
     i16x8* wp = reinterpret_cast<i16x8*>(ws + p.off_wp);
     const int64_t lanes = (int64_t)((H + 31) / 32) * p.NT * 64;
+    unsigned* ticket = reinterpret_cast<unsigned*>(ws + p.off_ticket);
     MOE_LAUNCH("k_pack_gate", k_pack_gate, dim3((unsigned)std::min<int64_t>(1024, (lanes + 255) / 256)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(wg), (int)H, (int)E, p.NT, wp);
+                       static_cast<const uint16_t*>(wg), (int)H, (int)E, p.NT, wp, p.stream ? ticket : nullptr);
     const dim3 grid(p.nblk);
     const uint16_t* xb = static_cast<const uint16_t*>(x);
+    if (p.stream) {
+#define MOE_FWDS(NTv, TGv)                                                                                        \
+  launch_fwd_stream<NTv, TGv>(p.nblk, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype,  \
+                              logits_out, lse_out, pc, pp, pz, ticket, aux_coef, z_coef, cnt_out, stats_out, aux_out, \
+                              z_out)
+      if (p.NT == 1) {
+        if (p.TG == 4) MOE_FWDS(1, 4);
+        else if (p.TG == 2) MOE_FWDS(1, 2);
+        else MOE_FWDS(1, 1);
+      } else {
+        if (p.TG == 4) MOE_FWDS(2, 4);
+        else if (p.TG == 2) MOE_FWDS(2, 2);
+        else MOE_FWDS(2, 1);
+      }
+#undef MOE_FWDS
+      return check_launch("k_router_fwd_bf16");
+    }
     switch (p.NT) {
       case 1: launch_fwd_mfma<1>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
       case 2: launch_fwd_mfma<2>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
