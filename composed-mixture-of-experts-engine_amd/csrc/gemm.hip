@@ -3,12 +3,17 @@
 // One kernel template covers the six products of the expert FFN forward and
 // backward.  Each computes C[m, n] = sum_k A[m, k] B[n, k] on
 // v_mfma_f32_32x32x16_bf16 with 256x256 block tiles (8 waves of 128x64) and
-// a 4-stage LDS ring (128 KB) of 32-wide k slices filled by LDS-DMA
-// (global_load_lds_dwordx4) about three stages ahead, so no operand passes
-// through VGPRs and each load has three compute slices to land.  The LDS reads
-// of each 16-wide k half overlap the MFMAs of the previous half.  Blocks are numbered
-// so that each XCD (blockIdx mod 8) runs a contiguous range of logical tiles:
-// tiles that share a weight panel stay in one L2.
+// a 2-stage LDS ring (128 KB) of 64-wide k slices filled by LDS-DMA
+// (global_load_lds_dwordx4), so no operand passes through VGPRs.  A 64-wide
+// slice makes every row of a k-contiguous operand one whole 128-byte line:
+// each DMA instruction fetches 8 full lines, which moves about 1.5x the bytes
+// per cycle of half-line (32-wide) slices through the CU's load path, the
+// path that bounds this kernel.  The refill of a slice is issued as soon as
+// every wave has read it and has a whole slice of MFMAs to land; the LDS
+// reads of each 16-wide k quarter overlap the MFMAs of the previous one, with
+// one workgroup barrier per slice.  Blocks are numbered so that each XCD
+// (blockIdx mod 8) runs a contiguous range of logical tiles: tiles that share
+// a weight panel stay in one L2.
 //
 //   operand mode 0 ("rows"): element (i, k) at P[i*ld + k]  (k contiguous);
 //                            MFMA fragments are 16-byte LDS reads
@@ -62,14 +67,14 @@ struct GemmArgs {
   int M, N, K;         // k-grouped: M, N fixed; row-grouped: N, K fixed
 };
 
-constexpr int GBM = 256, GBN = 256, GBK = 32, GSTAGES = 4;
+constexpr int GBM = 256, GBN = 256, GBK = 64;
+constexpr int GUNITS = 4;                 // LDS ring of operand tiles (unit 2s = A of stage s, 2s+1 = B)
 // Wave layouts (template parameter NW): 8 waves of 128x64 (2 x 4, two waves per SIMD) or 4 waves of
 // 128x128 (2 x 2, one wave per SIMD with up to 512 registers: a third fewer LDS bytes per MFMA).
 constexpr int GWM = 128;
-constexpr int GOPB = GBM * GBK * 2;       // bytes of one operand tile per stage (16 KB)
-constexpr int GSTAGE_B = 2 * GOPB;        // A + B per stage
+constexpr int GOPB = GBM * GBK * 2;       // bytes of one operand tile per stage (32 KB): one ring unit
 constexpr int GCP = GBN + 8;              // epilogue C tile pitch (elements)
-constexpr int GSMEM = (GSTAGES * GSTAGE_B > GBM * GCP * 2) ? GSTAGES * GSTAGE_B : GBM * GCP * 2;
+constexpr int GSMEM = (GUNITS * GOPB > GBM * GCP * 2) ? GUNITS * GOPB : GBM * GCP * 2;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
@@ -129,12 +134,13 @@ struct Interleave {
 
 // LDS tile layouts (per operand, per stage), both fed by LDS-DMA (lane l of a wave
 // instruction writes bytes [16l, 16l+16) of a 1 KB block):
-//   rows tile  [256 i][32 k]: row i is 64 bytes = 4 chunks of 8 k; chunk c sits in slot
-//              c ^ ((i >> 2) & 3)  -> 16-byte fragment reads are bank-conflict free.
-//   cols tile  [32 k][256 i]: row k is 512 bytes = 32 chunks of 8 i; chunk c sits in slot
+//   rows tile  [256 i][64 k]: row i is 128 bytes = 8 chunks of 8 k; chunk c sits in slot
+//              c ^ ((i >> 1) & 7)  -> the 16 rows one 16-lane group of a fragment read
+//              touches (same chunk) land in 16 distinct 16-byte bank groups.
+//   cols tile  [64 k][256 i]: row k is 512 bytes = 32 chunks of 8 i; chunk c sits in slot
 //              c ^ ((k & 3) << 2)  -> the four k-rows a transposing read touches fall in
 //              four disjoint 64-byte bank groups.
-__device__ __forceinline__ int rows_off(int i, int c) { return i * 64 + ((c ^ ((i >> 2) & 3)) << 4); }
+__device__ __forceinline__ int rows_off(int i, int c) { return i * 128 + ((c ^ ((i >> 1) & 7)) << 4); }
 __device__ __forceinline__ int cols_off(int k, int i) { return k * 512 + (((i >> 3) ^ ((k & 3) << 2)) << 4) + ((i & 7) << 1); }
 
 // Fragment (8 bf16) of a 32x32x16 MFMA operand: element j of lane l is (i = base + l%32, k = ks*16 + (l/32)*8 + j).
@@ -169,14 +175,18 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   const int wm0 = (wv / NW_N) * GWM;
   const int wn0 = (wv % NW_N) * GWN;
 
-  // ---- tile decode: XCD-contiguous logical order over a 1-D grid ----
-  const int P = gridDim.x;  // a multiple of 8
-  const int L = (int)(blockIdx.x & 7) * (P >> 3) + (int)(blockIdx.x >> 3);
-  int e, mbase, mlen, kbase, klen, nt;
+  // ---- tile decode: XCD-contiguous logical order over a 1-D grid.  The grid is sized for the most
+  // tiles any routing can produce; the real tile count is known only on the device, so it is split
+  // into 8 equal contiguous ranges (one per XCD: blockIdx mod 8), and the surplus blocks of every XCD
+  // exit at once. ----
+  const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
+  int L, e, mbase, mlen, kbase, klen, nt;
   if constexpr (GROUP == 0) {
     const int Tn = (EPI == 1) ? (2 * g.F + GBN - 1) / GBN : (g.N + GBN - 1) / GBN;
     const int total = g.tile_off[g.E] * Tn;
-    if (L >= total) return;
+    const int chunk = (total + 7) >> 3;
+    L = xcd * chunk + slot;
+    if (slot >= chunk || L >= total) return;
     int lo = 0, hi = g.E - 1;  // largest e with tile_off[e] * Tn <= L
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -194,11 +204,15 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     klen = g.K;
   } else {
     const int Tm = (g.M + GBM - 1) / GBM, Tn = (g.N + GBN - 1) / GBN;
-    if (L >= g.E * Tm * Tn) return;
+    const int total = g.E * Tm * Tn;
+    const int chunk = (total + 7) >> 3;
+    L = xcd * chunk + slot;
+    if (slot >= chunk || L >= total) return;
     e = L / (Tm * Tn);
     const int r = L - e * Tm * Tn;
     const int mt = r / Tn;
     nt = r - mt * Tn;
+
     mbase = mt * GBM;
     mlen = min(GBM, g.M - mbase);
     kbase = g.offsets[e];
@@ -209,33 +223,31 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   const int nk = (klen + GBK - 1) / GBK;
 
   // ---- per-lane DMA sources.  Wave instruction j (= QPW*wv + q, q < QPW) of an operand fills bytes
-  // [1024 j, 1024 j + 1024) of its stage tile: rows mode -> rows 16j + l/4, slot l%4;
-  // cols mode -> k-rows 2j + l/32, slot l%32.  Only the k offset of a stage varies in the loop:
-  // rows mode adds k0 elements, cols mode k0 * ld (a wave-uniform product). ----
+  // [1024 j, 1024 j + 1024) of its stage tile: rows mode -> rows 8j + l/8, slot l%8 (one whole
+  // 128-byte line per row); cols mode -> k-rows 2j + l/32, slot l%32.  Rows / columns past the
+  // tile are clamped to valid ones (their results are never stored), so a stage that lies wholly
+  // inside the reduction range needs only a wave-uniform step per instruction: rows mode adds k0
+  // elements, cols mode k0 * ld. ----
   const uint16_t* a_src[QPW];
   const uint16_t* b_src[QPW];
   const uint16_t* b_src2[QPW];
   int a_kl[QPW], b_kl[QPW];  // the lane's first k within a stage
-  bool a_ok[QPW], b_ok[QPW]; // the lane's row / column lies inside the tile
 #pragma unroll
   for (int q = 0; q < QPW; ++q) {
     const int j = QPW * wv + q;
     if constexpr (AMODE == 0) {
-      const int i = 16 * j + (lane >> 2);
-      a_kl[q] = ((lane & 3) ^ ((i >> 2) & 3)) * 8;
-      a_ok[q] = true;  // rows past the segment re-read its last row; their results are not stored
+      const int i = 8 * j + (lane >> 3);
+      a_kl[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
       a_src[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase + a_kl[q];
     } else {
       a_kl[q] = 2 * j + (lane >> 5);
       const int i = (((lane & 31) ^ ((a_kl[q] & 3) << 2)) << 3);
-      a_ok[q] = i < mlen;
-      a_src[q] = g.A + (int64_t)(kbase + a_kl[q]) * g.lda + mbase + i;
+      a_src[q] = g.A + (int64_t)(kbase + a_kl[q]) * g.lda + mbase + (i < mlen ? i : 0);
     }
     b_src2[q] = nullptr;
     if constexpr (BMODE == 0) {
-      const int i = 16 * j + (lane >> 2);
-      b_kl[q] = ((lane & 3) ^ ((i >> 2) & 3)) * 8;
-      b_ok[q] = true;
+      const int i = 8 * j + (lane >> 3);
+      b_kl[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
       const int ic = min(i, nlen - 1);
       if constexpr (EPI == 1) {
         const int f = nt * (GBN / 2) + (ic >> 6) * 32 + (ic & 31);
@@ -245,8 +257,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       }
     } else {
       b_kl[q] = 2 * j + (lane >> 5);
-      const int i = (((lane & 31) ^ ((b_kl[q] & 3) << 2)) << 3);
-      b_ok[q] = i < nlen;
+      int i = (((lane & 31) ^ ((b_kl[q] & 3) << 2)) << 3);
+      i = i < nlen ? i : 0;
       if constexpr (GROUP == 0) {
         b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)b_kl[q] * g.ldb + n0 + i;
         if (g.b_split > 0) b_src2[q] = g.B2 + (int64_t)e * g.b_estride + (int64_t)b_kl[q] * g.ldb + n0 + i;
@@ -256,24 +268,60 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     }
   }
 
-  auto issue = [&](int kt, uint8_t* st) {
-    const int k0 = min(kt, nk - 1) * GBK;
-    const int64_t a_step = AMODE == 0 ? (int64_t)k0 : (int64_t)k0 * g.lda;
+  // Refill a ring unit with the A (issue_a) or B (issue_b) tile of k slice kt.  Fast path (a
+  // wave-uniform branch): the slice lies inside the reduction range and on one side of b_split.
+  // Otherwise each lane checks its own k: past klen it reads 16 zero bytes, and cols-mode B switches
+  // to the second source at k = b_split.
+  auto issue_a = [&](int kt, uint8_t* unit) {
+    const int k0 = kt * GBK;
+    uint8_t* const sa = unit + QPW * wv * 1024;
+    const int64_t step = AMODE == 0 ? (int64_t)k0 : (int64_t)k0 * g.lda;
+    if (k0 + GBK <= klen) {
 #pragma unroll
-    for (int q = 0; q < QPW; ++q) {
-      const uint16_t* src = (a_ok[q] && k0 + a_kl[q] < klen) ? a_src[q] + a_step : g_zero16;
-      lds_dma16(src, lds_addr(st + (QPW * wv + q) * 1024));
-    }
-    // cols-mode B of the row-grouped products may switch source at k = b_split (a multiple of GBK,
-    // so a stage lies wholly on one side)
-    const bool second = BMODE == 1 && GROUP == 0 && g.b_split > 0 && k0 >= g.b_split;
-    const int kb = second ? k0 - g.b_split : k0;
-    const int64_t b_step = BMODE == 0 ? (int64_t)kb : (int64_t)kb * g.ldb;
+      for (int q = 0; q < QPW; ++q) lds_dma16(a_src[q] + step, lds_addr(sa + q * 1024));
+    } else {
 #pragma unroll
-    for (int q = 0; q < QPW; ++q) {
-      const uint16_t* src = (b_ok[q] && k0 + b_kl[q] < klen) ? (second ? b_src2[q] : b_src[q]) + b_step : g_zero16;
-      lds_dma16(src, lds_addr(st + GOPB + (QPW * wv + q) * 1024));
+      for (int q = 0; q < QPW; ++q)
+        lds_dma16(k0 + a_kl[q] < klen ? a_src[q] + step : g_zero16, lds_addr(sa + q * 1024));
     }
+  };
+  auto issue_b = [&](int kt, uint8_t* unit) {
+    const int k0 = kt * GBK;
+    const bool kfull = k0 + GBK <= klen;
+    uint8_t* const sb = unit + QPW * wv * 1024;
+    const int64_t bld = BMODE == 0 ? 1 : g.ldb;
+    bool split = false;
+    if constexpr (BMODE == 1 && GROUP == 0) split = g.b_split > 0 && k0 + GBK > g.b_split;
+    if (!split) {
+      const int64_t step = (int64_t)k0 * bld;
+      if (kfull) {
+#pragma unroll
+        for (int q = 0; q < QPW; ++q) lds_dma16(b_src[q] + step, lds_addr(sb + q * 1024));
+      } else {
+#pragma unroll
+        for (int q = 0; q < QPW; ++q)
+          lds_dma16(k0 + b_kl[q] < klen ? b_src[q] + step : g_zero16, lds_addr(sb + q * 1024));
+      }
+    } else {
+      const int64_t step1 = (int64_t)k0 * bld, step2 = (int64_t)(k0 - g.b_split) * bld;
+      if (kfull && k0 >= g.b_split) {
+#pragma unroll
+        for (int q = 0; q < QPW; ++q) lds_dma16(b_src2[q] + step2, lds_addr(sb + q * 1024));
+      } else {
+#pragma unroll
+        for (int q = 0; q < QPW; ++q) {
+          const int k = k0 + b_kl[q];
+          const uint16_t* src = k >= klen ? g_zero16 : (k < g.b_split ? b_src[q] + step1 : b_src2[q] + step2);
+          lds_dma16(src, lds_addr(sb + q * 1024));
+        }
+      }
+    }
+  };
+  // Ring unit u (A of slice u/2 when u is even, B otherwise) lives in LDS slot u % GUNITS.
+  auto unit_ptr = [&](int u) { return smem + (u & (GUNITS - 1)) * GOPB; };
+  auto issue_unit = [&](int u) {
+    if (u & 1) issue_b(u >> 1, unit_ptr(u));
+    else issue_a(u >> 1, unit_ptr(u));
   };
 
   f32x16 acc[MI][NI];
@@ -285,8 +333,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       for (int j = 0; j < 16; ++j) acc[mi][ni][j] = 0.f;
 
   // Fragments of one 16-wide k half of a stage, and the MFMAs that consume them.
-  auto frags = [&](const uint8_t* as, int ks, i16x8 (&fa)[MI], i16x8 (&fb)[NI]) {
-    const uint8_t* bs = as + GOPB;
+  auto frags = [&](const uint8_t* as, const uint8_t* bs, int ks, i16x8 (&fa)[MI], i16x8 (&fb)[NI]) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
       fa[mi] = AMODE == 0 ? frag_rows(as, wm0 + mi * 32, ks, lane) : frag_cols(as, wm0 + mi * 32, ks, lane);
@@ -302,35 +349,52 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, fa[mi]), __builtin_bit_cast(bf16x8, fb[ni]), acc[mi][ni]);
   };
 
-  // Software pipeline: the LDS reads of the next k half overlap the MFMAs of the current one.
-  // Iteration kt holds the first half of stage kt in registers on entry; the ring slot of stage kt
-  // is refilled with stage kt + GSTAGES once every wave has read its second half.
+  // Software pipeline over the four 16-wide k quarters of a stage: the LDS reads of quarter q+1 are
+  // interleaved with the MFMAs of quarter q (register sets 0 and 1 alternate).  Before the last
+  // quarter of stage kt every wave waits for stage kt+1 (the only DMA group in flight) and for its
+  // own reads of stage kt; one barrier makes both visible workgroup-wide, and stage kt's two units
+  // are refilled with stage kt+2 while the last quarter's MFMAs run.
   if (nk > 0) {
-#pragma unroll
-    for (int s = 0; s < GSTAGES; ++s) issue(s, smem + s * GSTAGE_B);
+    issue_unit(0);
+    issue_unit(1);
+    if (nk > 1) {
+      issue_unit(2);
+      issue_unit(3);
+    }
+    if (nk > 1) wait_vmcnt<2 * QPW>();  // this wave's part of stage 0 has landed
+    else wait_vmcnt<0>();
+    lds_barrier();                                   // every wave's part has
     i16x8 fa0[MI], fb0[NI], fa1[MI], fb1[NI];
-    wait_vmcnt<(GSTAGES - 1) * GDMA>();  // this wave's part of stage 0 has landed
-    lds_barrier();                       // every wave's part has
-    frags(smem, 0, fa0, fb0);
-    constexpr int NDS = (AMODE ? 2 : 1) * MI + (BMODE ? 2 : 1) * NI;  // LDS read instructions per k half
-    int slot = 0;
+    frags(unit_ptr(0), unit_ptr(1), 0, fa0, fb0);
+    constexpr int NDS = (AMODE ? 2 : 1) * MI + (BMODE ? 2 : 1) * NI;  // LDS read instructions per k quarter
     for (int kt = 0; kt < nk; ++kt) {
-      uint8_t* const cur = smem + slot * GSTAGE_B;  // ring slot of stage kt
-      slot = slot + 1 == GSTAGES ? 0 : slot + 1;
-      frags(cur, 1, fa1, fb1);
+      const uint8_t* const ca = unit_ptr(2 * kt);
+      const uint8_t* const cb = unit_ptr(2 * kt + 1);
+      frags(ca, cb, 1, fa1, fb1);
       mma(fa0, fb0);
       Interleave<0, MI * NI, MI * NI / 2, NDS, 0>::run();
       __builtin_amdgcn_sched_barrier(0);
-      wait_vmcnt_lgkm0<(GSTAGES - 2) * GDMA>();  // stage kt+1 landed; this wave's reads of slot kt are done
+      frags(ca, cb, 2, fa0, fb0);
+      mma(fa1, fb1);
+      Interleave<0, MI * NI, MI * NI / 2, NDS, 0>::run();
+      __builtin_amdgcn_sched_barrier(0);
+      frags(ca, cb, 3, fa1, fb1);
+      mma(fa0, fb0);
+      Interleave<0, MI * NI, MI * NI / 2, NDS, 0>::run();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt_lgkm0<0>();  // stage kt+1 landed; this wave's reads of stage kt are done
       lds_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      issue(kt + GSTAGES, cur);                  // clamped past the end: re-reads the last stage, never read back
-      frags(smem + slot * GSTAGE_B, 0, fa0, fb0);
+      if (kt + 2 < nk) {
+        issue_unit(2 * kt + 4);
+        issue_unit(2 * kt + 5);
+      }
+      if (kt + 1 < nk) frags(unit_ptr(2 * kt + 2), unit_ptr(2 * kt + 3), 0, fa0, fb0);
       mma(fa1, fb1);
-      Interleave<0, MI * NI, MI * NI / 2, NDS, GDMA>::run();
+      Interleave<0, MI * NI, MI * NI / 2, NDS, 0>::run();
       __builtin_amdgcn_sched_barrier(0);
     }
-    wait_vmcnt<0>();  // the clamped refills land before the epilogue reuses the ring
+    wait_vmcnt<0>();
   }
   __syncthreads();
 
