@@ -302,18 +302,36 @@ __global__ __launch_bounds__(256) void k_router_fwd_bf16(
   }
 }
 
+// Per-block partials handed to the last block of the same launch.  They are stored and loaded as
+// agent-scope relaxed atomics: the stores write through the XCD-local L2 to the coherence point and the
+// loads bypass it, so no L2 writeback / invalidate (buffer_wbl2 / buffer_inv) is needed around the ticket
+// -- those flush every dirty line of the L2, including data earlier kernels left there.
+template <typename T>
+__device__ __forceinline__ void st_part(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH, typename T>
+__device__ __forceinline__ T ld_part(const T* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+
 // ---------------------------------------------------------------------------
 // Finalize: fixed-order sums of the per-block partials -> cnt, stats, aux, z (one block of NTHR threads).
 // ---------------------------------------------------------------------------
+// LDS scratch the finalize needs (floats).
 template <int NTHR>
+constexpr int finalize_scratch_floats() { return 2 * kMaxE + 2 * (NTHR / 64); }
+
+template <int NTHR, bool COH = false>
 __device__ __forceinline__ void router_finalize_block(const int* __restrict__ part_cnt, const float* __restrict__ part_p,
                                                       const float* __restrict__ part_z, int nblk, int N, int E, int K,
                                                       float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
                                                       float* __restrict__ stats, float* __restrict__ aux_out,
-                                                      float* __restrict__ z_out) {
-  __shared__ float s_c[kMaxE];
-  __shared__ float s_pe[kMaxE];
-  __shared__ float s_red[2][NTHR / 64];
+                                                      float* __restrict__ z_out, float* scratch) {
+  float* s_c = scratch;                                                       // [kMaxE]
+  float* s_pe = scratch + kMaxE;                                              // [kMaxE]
+  float(*s_red)[NTHR / 64] = reinterpret_cast<float(*)[NTHR / 64]>(scratch + 2 * kMaxE);  // [2][NTHR/64]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // threads per expert: a power of two <= 64 so each expert's threads sit in one wave
@@ -332,8 +350,8 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
         float pv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          cv[u] = part_cnt[(int64_t)(b + u * tpe) * E + e];
-          pv[u] = part_p[(int64_t)(b + u * tpe) * E + e];
+          cv[u] = ld_part<COH>(&part_cnt[(int64_t)(b + u * tpe) * E + e]);
+          pv[u] = ld_part<COH>(&part_p[(int64_t)(b + u * tpe) * E + e]);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -342,8 +360,8 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
         }
       }
       for (; b < nblk; b += tpe) {
-        c += part_cnt[(int64_t)b * E + e];
-        p += part_p[(int64_t)b * E + e];
+        c += ld_part<COH>(&part_cnt[(int64_t)b * E + e]);
+        p += ld_part<COH>(&part_p[(int64_t)b * E + e]);
       }
     }
     for (int o = tpe / 2; o > 0; o >>= 1) {
@@ -365,8 +383,8 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
       float nn[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        zz[u] = part_z[2 * (b + u * NTHR)];
-        nn[u] = part_z[2 * (b + u * NTHR) + 1];
+        zz[u] = ld_part<COH>(&part_z[2 * (b + u * NTHR)]);
+        nn[u] = ld_part<COH>(&part_z[2 * (b + u * NTHR) + 1]);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -375,8 +393,8 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
       }
     }
     for (; b < nblk; b += NTHR) {
-      z += part_z[2 * b];
-      nf += part_z[2 * b + 1];
+      z += ld_part<COH>(&part_z[2 * b]);
+      nf += ld_part<COH>(&part_z[2 * b + 1]);
     }
   }
   z = wave_sum(z);
@@ -423,47 +441,104 @@ __global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__
                                                          int K, float aux_coef, float z_coef,
                                                          int64_t* __restrict__ cnt_out, float* __restrict__ stats,
                                                          float* __restrict__ aux_out, float* __restrict__ z_out) {
-  router_finalize_block<256>(part_cnt, part_p, part_z, nblk, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out, z_out);
+  __shared__ float scratch[finalize_scratch_floats<256>()];
+  router_finalize_block<256>(part_cnt, part_p, part_z, nblk, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out, z_out,
+                             scratch);
 }
 
 // ---------------------------------------------------------------------------
 // Forward, streaming form (bf16 x bf16, E <= 32, H % 256 == 0).  Block = 8 waves = TG groups of 16 tokens.
-// Wave w streams the 32-wide hidden chunks w, w + 8, w + 16, ... of all the block's tokens, so every
-// packed-gate fragment it loads serves TG token groups; U chunks per prefetch group, double-buffered and
-// branch-free.  The 8 partial logit tiles are summed in LDS in wave order, waves 0 .. TG-1 route one group
-// each, and the block's partial statistics go to part_*.  The last block to finish (ticket counter, reset
-// by k_pack_gate before the launch) folds all blocks' partials: the finalize needs no launch of its own.
+// The block's 16*TG token rows are streamed through a ring of kFwdSlots LDS slots, one 256-column slice per
+// slot, by LDS-DMA with whole 128-byte lines and the streaming cache policy (sc1 nt: the tokens are read
+// once); the matching 256 rows of the raw gate [H, E] ride along in the same slot, so the gate needs no
+// packing pass.  Wave w owns the 32-column chunk w of every slice for all TG groups: its MFMA A fragments
+// are 16-byte LDS reads (x tile rows are XOR-swizzled in 16-byte units, so the 16 rows one read touches hit
+// 16 different bank groups) and its B fragments are gathered from the gate rows.  The 8 partial logit tiles
+// are summed in LDS in wave order, waves 0 .. TG-1 route one group each, and the block's partial statistics
+// go to part_*.  The last block to finish (ticket counter: zero on entry, reset to zero by that block) folds
+// all blocks' partials, so the finalize needs no launch of its own.
 // ---------------------------------------------------------------------------
-template <int NT, int TG, int U>
+
+typedef __attribute__((address_space(3))) void lds_void_r;
+__device__ __forceinline__ uint32_t lds_addr_r(const void* p) { return (uint32_t)(uintptr_t)(lds_void_r*)p; }
+
+// One 16-byte-per-lane LDS-DMA with the streaming cache policy.  Issued from asm so the compiler does not
+// make the LDS reads of other slots wait for it; completion is ordered by explicit vmcnt waits.
+__device__ __forceinline__ void lds_dma16_stream(const void* src, uint32_t lds) {
+  __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off sc1 nt" : : "v"(src), "{m0}"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void router_wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int NT, int TG>
 __global__ __launch_bounds__(512) void k_router_fwd_stream(
-    const uint16_t* __restrict__ x, const i16x8* __restrict__ wp, const float* __restrict__ bias, int N, int H,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, const float* __restrict__ bias, int N, int H,
     int E, int K, int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
     float* __restrict__ lse_out, int* __restrict__ part_cnt, float* __restrict__ part_p, float* __restrict__ part_z,
     unsigned* __restrict__ ticket, float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
     float* __restrict__ stats, float* __restrict__ aux_out, float* __restrict__ z_out) {
-  __shared__ f32x4 s_acc[8][TG][NT][64];
-  __shared__ int s_cnt[NT * 16];
-  __shared__ float s_p[TG][NT * 16];
-  __shared__ float s_z[TG];
-  __shared__ int s_nf[TG];
-  __shared__ int s_last;
+  constexpr int ROWS = 16 * TG;
+  constexpr int XB = ROWS * 512;    // x tile of one slice: ROWS rows x 256 columns (bf16)
+  constexpr int GI = NT;            // gate DMA instructions per wave per slice (1 KB each)
+  constexpr int GB = 8 * GI * 1024; // gate tile region: 256 rows x E <= 16 * NT experts (bf16), padded
+  constexpr int SLOT = XB + GB;
+  constexpr int XI = ROWS / 16;     // x DMA instructions per wave per slice (2 rows x 512 B each)
+  constexpr int GPS = XI + GI;      // DMA instructions per wave per slice
+  // ring depth: 4 slots (3 slices in flight) fill the 160 KB LDS with NT == 1; NT == 2 fits 3
+  constexpr int kFwdSlots = NT == 1 ? 4 : 3;
+  static_assert(kFwdSlots <= 4, "the waits below cover at most two slices ahead");
+  constexpr int RING = kFwdSlots * SLOT;
+  // after the stream the ring holds the partial logit tiles and the epilogue's small arrays
+  constexpr int ACC = 8 * TG * NT * 64 * 16;
+  constexpr int O_CNT = ACC, O_P = O_CNT + NT * 16 * 4, O_Z = O_P + TG * NT * 16 * 4, O_NF = O_Z + TG * 4;
+  constexpr int O_LAST = O_NF + TG * 4, O_FIN = O_LAST + 16;
+  constexpr int EPI = O_FIN + finalize_scratch_floats<512>() * 4;
+  static_assert(RING >= EPI, "ring too small for the epilogue arrays");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING];
+  f32x4(*s_acc)[TG][NT][64] = reinterpret_cast<f32x4(*)[TG][NT][64]>(ring);
+  int* s_cnt = reinterpret_cast<int*>(ring + O_CNT);
+  float(*s_p)[NT * 16] = reinterpret_cast<float(*)[NT * 16]>(ring + O_P);
+  float* s_z = reinterpret_cast<float*>(ring + O_Z);
+  int* s_nf = reinterpret_cast<int*>(ring + O_NF);
+  int& s_last = *reinterpret_cast<int*>(ring + O_LAST);
+  float* s_fin = reinterpret_cast<float*>(ring + O_FIN);
 
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4;
   const int n = lane & 15;
-  const int t0 = blockIdx.x * (16 * TG);
-  for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
+  const int t0 = blockIdx.x * ROWS;
 
-  // lane (g, n) of group q loads row t0 + 16q + n (clamped), k = 32c + 8g .. +8 of chunk c: the A fragment
-  const i16x8* xr[TG];
+  // x DMA: instruction j (= XI*wv + q) of a slice fills rows 2j, 2j+1 (lanes 0-31 / 32-63): lane slot
+  // u' = lane%32 holds the row's 16-byte unit u = u' ^ (row & 31) of the slice (rows past N re-read row N-1)
+  const uint16_t* xsrc[XI];
 #pragma unroll
-  for (int q = 0; q < TG; ++q) {
-    const int row = min(t0 + 16 * q + n, N - 1);
-    xr[q] = reinterpret_cast<const i16x8*>(x + (int64_t)row * H) + g;
+  for (int q = 0; q < XI; ++q) {
+    const int row = 2 * (XI * wv + q) + (lane >> 5);
+    const int u = (lane & 31) ^ (row & 31);
+    xsrc[q] = x + (int64_t)min(t0 + row, N - 1) * H + u * 8;
   }
-  const i16x8* wb = wp + lane;
-  const int nci = H >> 8;  // chunks per wave
+  // gate DMA: the slice's 256 gate rows are 512*E contiguous bytes; instruction j (= GI*wv + q) copies
+  // bytes [1024 j, 1024 j + 1024) of them, lanes past the end re-read the slice start (never used)
+  const int gbytes = 512 * E;
+  int gofs[GI];
+#pragma unroll
+  for (int q = 0; q < GI; ++q) {
+    const int b = (GI * wv + q) * 1024 + lane * 16;
+    gofs[q] = b < gbytes ? b : 0;
+  }
+  const int nsl = H >> 8;
+  auto slot_ptr = [&](int sl) { return ring + (sl % kFwdSlots) * SLOT; };
+  auto issue = [&](int sl) {
+    uint8_t* const sp = slot_ptr(sl);
+#pragma unroll
+    for (int q = 0; q < XI; ++q) lds_dma16_stream(xsrc[q] + sl * 256, lds_addr_r(sp + (XI * wv + q) * 1024));
+    const uint8_t* gsrc = reinterpret_cast<const uint8_t*>(wg) + (int64_t)sl * gbytes;
+#pragma unroll
+    for (int q = 0; q < GI; ++q) lds_dma16_stream(gsrc + gofs[q], lds_addr_r(sp + XB + (GI * wv + q) * 1024));
+  };
 
   f32x4 acc[TG][NT];
 #pragma unroll
@@ -471,67 +546,51 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[q][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  i16x8 a0[U][TG], a1[U][TG], b0[U][NT], b1[U][NT];
-  auto load_grp = [&](i16x8(&a)[U][TG], i16x8(&b)[U][NT], int i) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = wv + 8 * (i + u);
-#pragma unroll
-      for (int q = 0; q < TG; ++q) a[u][q] = __builtin_nontemporal_load(xr[q] + c * 4);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) b[u][nt] = wb[(c * NT + nt) * 64];
-    }
-  };
-  auto mma_grp = [&](const i16x8(&a)[U][TG], const i16x8(&b)[U][NT]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int q = 0; q < TG; ++q)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          acc[q][nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a[u][q]), __builtin_bit_cast(bf16x8, b[u][nt]),
-                                    acc[q][nt]);
-  };
-  // the scheduling barriers keep the order "issue the next group's loads, then the MFMAs of the current
-  // group": left free, the scheduler interleaves them and the waits then drain the prefetch
-  int i = 0;
-  const int npair = nci / (2 * U);
-  if (npair > 0) {
-    load_grp(a0, b0, 0);
-    for (int pr = 0; pr < npair - 1; ++pr) {
-      load_grp(a1, b1, i + U);
-      __builtin_amdgcn_sched_barrier(0);
-      mma_grp(a0, b0);
-      __builtin_amdgcn_sched_barrier(0);
-      load_grp(a0, b0, i + 2 * U);
-      __builtin_amdgcn_sched_barrier(0);
-      mma_grp(a1, b1);
-      __builtin_amdgcn_sched_barrier(0);
-      i += 2 * U;
-    }
-    load_grp(a1, b1, i + U);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_grp(a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_grp(a1, b1);
-    i += 2 * U;
-  }
-  for (; i < nci; ++i) {
-    const int c = wv + 8 * i;
+  for (int sl = 0; sl < kFwdSlots - 1; ++sl)
+    if (sl < nsl) issue(sl);
+  for (int sl = 0; sl < nsl; ++sl) {
+    // slice sl has landed: only the slices issued after it (min(kFwdSlots - 2, nsl - 1 - sl)) may be pending
+    const int ahead = min(kFwdSlots - 2, nsl - 1 - sl);
+    if (ahead >= 2) router_wait_vmcnt<2 * GPS>();
+    else if (ahead == 1) router_wait_vmcnt<GPS>();
+    else router_wait_vmcnt<0>();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's part of slice sl is in LDS; every wave is done with slice sl-1
+    __asm__ volatile("" ::: "memory");
+    if (sl + kFwdSlots - 1 < nsl) issue(sl + kFwdSlots - 1);  // into the slot of slice sl-1
+    const uint8_t* const sp = slot_ptr(sl);
+    i16x8 a[TG], b[NT];
 #pragma unroll
     for (int q = 0; q < TG; ++q) {
-      const i16x8 a = __builtin_nontemporal_load(xr[q] + c * 4);
+      const int row = 16 * q + n;
+      const int u = 4 * wv + g;
+      a[q] = *reinterpret_cast<const i16x8*>(sp + row * 512 + ((u ^ (row & 31)) << 4));
+    }
+    const uint16_t* gt = reinterpret_cast<const uint16_t*>(sp + XB);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int e = nt * 16 + n;
+      const int ec = min(e, E - 1);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const short v = (short)gt[(32 * wv + 8 * g + j) * E + ec];
+        b[nt][j] = e < E ? v : (short)0;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < TG; ++q)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
-        acc[q][nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, wb[(c * NT + nt) * 64]),
-                                  acc[q][nt]);
-    }
+        acc[q][nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a[q]), __builtin_bit_cast(bf16x8, b[nt]), acc[q][nt]);
   }
+  __syncthreads();  // every wave is done with the ring: it now holds the partial logit tiles
 
 #pragma unroll
   for (int q = 0; q < TG; ++q)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) s_acc[wv][q][nt][lane] = acc[q][nt];
+  for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
   __syncthreads();  // partial tiles visible, s_cnt zeroed
   if (wv < TG) {
     f32x4 lg[NT];
@@ -549,8 +608,8 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
     float p = 0.f;
 #pragma unroll
     for (int q = 0; q < TG; ++q) p += s_p[q][e];
-    part_cnt[(int64_t)blockIdx.x * E + e] = s_cnt[e];
-    part_p[(int64_t)blockIdx.x * E + e] = p;
+    st_part(&part_cnt[(int64_t)blockIdx.x * E + e], s_cnt[e]);
+    st_part(&part_p[(int64_t)blockIdx.x * E + e], p);
   }
   if (threadIdx.x == 0) {
     float z = 0.f;
@@ -560,22 +619,22 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
       z += s_z[q];
       nfs += s_nf[q];
     }
-    part_z[2 * blockIdx.x] = z;
-    part_z[2 * blockIdx.x + 1] = (float)nfs;
+    st_part(&part_z[2 * blockIdx.x], z);
+    st_part(&part_z[2 * blockIdx.x + 1], (float)nfs);
   }
-  // ---- the last block folds every block's partials.  The barrier orders every thread's partial stores
-  // before thread 0's agent-scope release (cumulative), so one fence per block publishes them; the last
-  // block's acquire makes all blocks' partials visible to it. ----
+  // ---- the last block folds every block's partials.  The partials are write-through stores; every
+  // thread waits for its own to complete (s_waitcnt: a workgroup barrier alone does not wait for global
+  // stores), so after the barrier they are all at the coherence point before thread 0's ticket
+  // increment, and the last block reads them past the L2. ----
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (threadIdx.x == 0)
     s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-  }
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  router_finalize_block<512>(part_cnt, part_p, part_z, gridDim.x, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out,
-                             z_out);
+  router_finalize_block<512, true>(part_cnt, part_p, part_z, gridDim.x, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out,
+                                   z_out, s_fin);
   if (threadIdx.x == 0) *ticket = 0u;
 }
 
@@ -1240,13 +1299,13 @@ struct FwdPlan {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
+FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt, bool allow_stream = true) {
   FwdPlan p{};
   p.mfma = x_dt == MOE_BF16 && w_dt == MOE_BF16 && H % 32 == 0 && E <= 128;
   p.NT = (int)((E + 15) / 16);
   if (p.NT == 3) p.NT = 4;
   if (p.NT > 4 && p.NT < 8) p.NT = 8;
-  p.stream = p.mfma && E <= 32 && H % 256 == 0;
+  p.stream = allow_stream && p.mfma && E <= 32 && H % 256 == 0;
   if (p.stream) {
     // 16 * TG tokens per block: the largest TG that still gives one block per CU (256)
     p.TG = N >= 256 * 64 ? 4 : (N >= 256 * 32 ? 2 : 1);
@@ -1256,7 +1315,11 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   } else {
     p.nblk = (int)std::min<int64_t>(512, std::max<int64_t>(1, (N + 15) / 16));
   }
+  // the ticket word sits at offset 0 in every layout: calls that reuse one workspace with different
+  // shapes or paths never write over it, and each streaming call leaves it at zero
   size_t off = 0;
+  p.off_ticket = off;
+  off += 256;
   p.off_wp = off;
   off += p.mfma ? align256((size_t)((H + 31) / 32) * p.NT * 64 * 16) : 0;
   p.off_cnt = off;
@@ -1265,8 +1328,6 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   off += align256((size_t)p.nblk * E * sizeof(float));
   p.off_z = off;
   off += align256((size_t)p.nblk * 2 * sizeof(float));
-  p.off_ticket = off;
-  off += 256;
   p.total = off;
   return p;
 }
@@ -1330,12 +1391,11 @@ void launch_reduce(hipStream_t s, const float* ws, int nchunk, int64_t len, void
 }
 
 template <int NT, int TG>
-void launch_fwd_stream(int nblk, hipStream_t s, const uint16_t* x, const i16x8* wp, const float* bias, int N, int H,
+void launch_fwd_stream(int nblk, hipStream_t s, const uint16_t* x, const uint16_t* wg, const float* bias, int N, int H,
                        int E, int K, int64_t* idx, void* w, int w_dt, float* logits, float* lse, int* pc, float* pp,
                        float* pz, unsigned* ticket, float aux_coef, float z_coef, int64_t* cnt, float* stats,
                        float* aux_out, float* z_out) {
-  constexpr int U = 4;
-  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_stream<NT, TG, U>), dim3(nblk), dim3(512), 0, s, x, wp, bias, N, H, E, K,
+  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_stream<NT, TG>), dim3(nblk), dim3(512), 0, s, x, wg, bias, N, H, E, K,
              idx, w, w_dt, logits, lse, pc, pp, pz, ticket, aux_coef, z_coef, cnt, stats, aux_out, z_out);
 }
 
@@ -1371,7 +1431,7 @@ using namespace moe;
 extern "C" size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype) {
   (void)K;
   if (N <= 0 || H <= 0 || E <= 0) return 0;
-  return plan_fwd(N, H, E, x_dtype, wg_dtype).total;
+  return std::max(plan_fwd(N, H, E, x_dtype, wg_dtype).total, plan_fwd(N, H, E, x_dtype, wg_dtype, false).total);
 }
 
 extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias, int64_t N,
@@ -1389,7 +1449,8 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
   if (N == 0) return 0;
   if (!x || !wg || !idx_out || !w_out || !logits_out || !lse_out || !cnt_out || !stats_out)
     return fail_arg("moe_router_fwd: null pointer argument");
-  const FwdPlan p = plan_fwd(N, H, E, x_dtype, wg_dtype);
+  // the streaming form DMAs the gate rows too, so it needs both operands 16-byte aligned
+  const FwdPlan p = plan_fwd(N, H, E, x_dtype, wg_dtype, aligned16(x) && aligned16(wg));
   if (ws_bytes < p.total || (!workspace && p.total))
     return set_error("moe_router_fwd: workspace %zu < %zu bytes", ws_bytes, p.total), MOE_EWORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -1398,31 +1459,34 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
   float* pp = reinterpret_cast<float*>(ws + p.off_p);
   float* pz = reinterpret_cast<float*>(ws + p.off_z);
   const bool mfma = p.mfma && aligned16(x);
+  if (mfma && p.stream) {
+    // streaming form: raw gate, finalize folded into the last block (ticket zero on entry and on exit)
+    unsigned* ticket = reinterpret_cast<unsigned*>(ws + p.off_ticket);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const uint16_t* wb = static_cast<const uint16_t*>(wg);
+#define MOE_FWDS(NTv, TGv)                                                                                        \
+  launch_fwd_stream<NTv, TGv>(p.nblk, s, xb, wb, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype,  \
+                              logits_out, lse_out, pc, pp, pz, ticket, aux_coef, z_coef, cnt_out, stats_out, aux_out, \
+                              z_out)
+    if (p.NT == 1) {
+      if (p.TG == 4) MOE_FWDS(1, 4);
+      else if (p.TG == 2) MOE_FWDS(1, 2);
+      else MOE_FWDS(1, 1);
+    } else {
+      if (p.TG == 4) MOE_FWDS(2, 4);
+      else if (p.TG == 2) MOE_FWDS(2, 2);
+      else MOE_FWDS(2, 1);
+    }
+#undef MOE_FWDS
+    return check_launch("k_router_fwd_bf16");
+  }
   if (mfma) {
     i16x8* wp = reinterpret_cast<i16x8*>(ws + p.off_wp);
     const int64_t lanes = (int64_t)((H + 31) / 32) * p.NT * 64;
-    unsigned* ticket = reinterpret_cast<unsigned*>(ws + p.off_ticket);
     MOE_LAUNCH("k_pack_gate", k_pack_gate, dim3((unsigned)std::min<int64_t>(1024, (lanes + 255) / 256)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(wg), (int)H, (int)E, p.NT, wp, p.stream ? ticket : nullptr);
+                       static_cast<const uint16_t*>(wg), (int)H, (int)E, p.NT, wp, nullptr);
     const dim3 grid(p.nblk);
     const uint16_t* xb = static_cast<const uint16_t*>(x);
-    if (p.stream) {
-#define MOE_FWDS(NTv, TGv)                                                                                        \
-  launch_fwd_stream<NTv, TGv>(p.nblk, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype,  \
-                              logits_out, lse_out, pc, pp, pz, ticket, aux_coef, z_coef, cnt_out, stats_out, aux_out, \
-                              z_out)
-      if (p.NT == 1) {
-        if (p.TG == 4) MOE_FWDS(1, 4);
-        else if (p.TG == 2) MOE_FWDS(1, 2);
-        else MOE_FWDS(1, 1);
-      } else {
-        if (p.TG == 4) MOE_FWDS(2, 4);
-        else if (p.TG == 2) MOE_FWDS(2, 2);
-        else MOE_FWDS(2, 1);
-      }
-#undef MOE_FWDS
-      return check_launch("k_router_fwd_bf16");
-    }
     switch (p.NT) {
       case 1: launch_fwd_mfma<1>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;
       case 2: launch_fwd_mfma<2>(grid, s, xb, wp, bias, (int)N, (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz); break;

@@ -155,5 +155,23 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+_ws_cache = {}
+
+
+def workspace(nbytes: int, device: torch.device, key: Optional[str] = None) -> torch.Tensor:
+    """Scratch memory for one call.  With ``key``, a workspace that must start zeroed and that the kernels
+    leave zeroed where it matters (the router forward's ticket counter): one zero-initialised buffer per
+    (key, device, stream), reused by every call on that stream (stream order serialises them).  Under
+    graph capture a fresh zeroed buffer is made instead, so each replay zeroes it again."""
+    n = max(int(nbytes), 1)
+    if key is None:
+        return torch.empty(n, dtype=torch.uint8, device=device)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(n, dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    k = (key, device.index, stream)
+    buf = _ws_cache.get(k)
+    if buf is None or buf.numel() < n:
+        buf = torch.zeros(n, dtype=torch.uint8, device=device)
+        _ws_cache[k] = buf
+    return buf

@@ -63,7 +63,7 @@ def router_forward(
             return idx, w, logits, lse, cnt, stats, aux, z
         return idx, w, logits, lse, cnt, stats
     nbytes = lib.moe_router_fwd_workspace(N, H, E, k, xdt, wdt)
-    ws = L.workspace(nbytes, dev)
+    ws = L.workspace(nbytes, dev, key="router_fwd")  # zeroed once; the kernel leaves its ticket at zero
     rc = lib.moe_router_fwd(
         x.data_ptr(), xdt, gate_w.data_ptr(), wdt, L.ptr(bias), N, H, E, k,
         idx.data_ptr(), w.data_ptr(), odt, logits.data_ptr(), lse.data_ptr(),

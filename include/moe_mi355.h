@@ -82,6 +82,10 @@ int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
  *   aux_out  [1] f32 or NULL: aux_coef * stats[1] (load-balance loss)
  *   z_out    [1] f32 or NULL: z_coef * stats[0]   (z-loss)
  * Limits: 1 <= K <= min(E, 32), 1 <= E <= 256.
+ * Workspace: zero it before its first use and reuse it for later calls on
+ * the same stream.  Its first word is a completion counter that the call
+ * expects at zero and leaves at zero (no other part of the library writes
+ * it); calls that share a workspace must not overlap.
  * ---------------------------------------------------------------------- */
 size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
 int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias,
