@@ -1074,8 +1074,14 @@ typedef __attribute__((address_space(3))) sh4 lds_sh4;
 template <int NTE>
 __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ wg,
-                                                            const uint16_t* __restrict__ gb, int N, int H, int E,
-                                                            int tc_len, int nht, uint16_t* __restrict__ dx,
+                                                            const float* __restrict__ logits,
+                                                            const int64_t* __restrict__ idx,
+                                                            const void* __restrict__ gw, int gw_dt,
+                                                            const int64_t* __restrict__ cnt,
+                                                            const float* __restrict__ grad_aux,
+                                                            const float* __restrict__ grad_z, float aux_coef,
+                                                            float z_coef, int N, int H, int E, int K, int tc_len,
+                                                            int nht, uint16_t* __restrict__ dx,
                                                             float* __restrict__ ws_dw) {
   constexpr int GP = 32 + 8;         // token-major G row pitch (32 expert slots)
   constexpr int GTP = kSTC + 8;      // expert-major G row pitch
@@ -1110,18 +1116,35 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
   load_x(xa, tbeg);
   load_x(xb, tbeg + 32);
 
-  // ---- stage the chunk's G (bf16, [N, 32] zero-padded rows) in both layouts; rows past the chunk are 0 ----
-  for (int q = tid; q < nst * 32 * 4; q += 256) {  // 4 x 16 bytes per token row
-    const int r = q >> 2, c8 = (q & 3) * 8;
+  // ---- G = dL/dlogits of the chunk, one token per thread (the x prefetch above is in flight meanwhile),
+  // rounded to bf16 as the reference does (grad_logits.to(tokens.dtype)) and staged in both layouts; rows
+  // past the chunk are 0 ----
+  {
+    const GCoef cf = glogit_coef(grad_aux, grad_z, aux_coef, z_coef, N, E, K);
+    const int r = tid;  // blockDim == kSTC >= the chunk's rounded-up row count
     const int t = tbeg + r;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(gb + (int64_t)min(t, tend - 1) * 32 + c8);
-    const bool ok = t < tend;
-    const u32x4 w = u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
-    *reinterpret_cast<u32x4*>(&gs[r * GP + c8]) = w;
+    float gl[NTE * 16];
+    if (t < tend) {
+      glogit_token<1, NTE * 16>(logits, idx, gw, gw_dt, cnt, cf, t, E, K, 0, gl);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = c8 + j;
-      if (e < NTE * 16) gts[e * GTP + r] = (uint16_t)(w[j >> 1] >> ((j & 1) * 16));
+      for (int e = 0; e < NTE * 16; ++e) gl[e] = 0.f;
+    }
+    if (r < nst * 32) {
+#pragma unroll
+      for (int c8 = 0; c8 < 32; c8 += 8) {
+        u32x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e0 = c8 + 2 * j, e1 = e0 + 1;
+          const float v0 = (e0 < NTE * 16 && e0 < E) ? gl[e0 < NTE * 16 ? e0 : 0] : 0.f;
+          const float v1 = (e1 < NTE * 16 && e1 < E) ? gl[e1 < NTE * 16 ? e1 : 0] : 0.f;
+          w[j] = pack2bf(v0, v1);
+        }
+        *reinterpret_cast<u32x4*>(&gs[r * GP + c8]) = w;
+      }
+#pragma unroll
+      for (int e = 0; e < NTE * 16; ++e) gts[e * GTP + r] = e < E ? f2bf(gl[e]) : (uint16_t)0;
     }
   }
 
@@ -1255,16 +1278,31 @@ __global__ __launch_bounds__(256) void k_reduce_chunks(const float* __restrict__
 #pragma unroll
     for (int v = 0; v < VEC; ++v) a[v] = 0.f;
     if (q < ngroups && ws != nullptr) {
-      for (int c = cg; c < nchunk; c += 4) {
-        const float* src = ws + (int64_t)c * len + q * VEC;
-        if constexpr (VEC == 4) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(src);
+      // chunks cg, cg+4, ... summed in that order; loaded 8 at a time so the loads overlap
+      int c = cg;
+      for (; c + 28 < nchunk; c += 32) {
+        float xv[8][VEC];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) a[v] += x[v];
-        } else {
+        for (int u = 0; u < 8; ++u) {
+          const float* src = ws + (int64_t)(c + 4 * u) * len + q * VEC;
+          if constexpr (VEC == 4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(src);
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) a[v] += src[v];
+            for (int v = 0; v < 4; ++v) xv[u][v] = x[v];
+          } else {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) xv[u][v] = src[v];
+          }
         }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) a[v] += xv[u][v];
+      }
+      for (; c < nchunk; c += 4) {
+        const float* src = ws + (int64_t)c * len + q * VEC;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) a[v] += src[v];
       }
     }
 #pragma unroll
@@ -1368,7 +1406,7 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   }
   if (p.nchunk < 1) p.nchunk = 1;
   size_t off = 0;
-  p.off_g = off;
+  p.off_g = off;  // G (and its bf16 copy) for the non-streaming paths, which an unaligned call falls back to
   off += align256((size_t)N * E * sizeof(float));
   p.off_gb = off;
   off += p.mfma ? align256((size_t)N * p.EK * 32 * sizeof(uint16_t)) : 0;
@@ -1410,11 +1448,13 @@ void launch_fwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const i16x8* w
 }
 
 template <int NTE>
-void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, const uint16_t* gb, int N, int H, int E,
-                        int tc_len, int nchunk, uint16_t* dx, float* ws) {
+void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, const float* logits, const int64_t* idx,
+                        const void* gw, int gw_dt, const int64_t* cnt, const float* grad_aux, const float* grad_z,
+                        float aux_coef, float z_coef, int N, int H, int E, int K, int tc_len, int nchunk, uint16_t* dx,
+                        float* ws) {
   const int nht = H / 256;
-  MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)), dim3(256), 0, s, x, wg, gb,
-             N, H, E, tc_len, nht, dx, ws);
+  MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)), dim3(256), 0, s, x, wg,
+             logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K, tc_len, nht, dx, ws);
 }
 
 template <int EK, int NTE>
@@ -1554,6 +1594,22 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
   float* wsdw = reinterpret_cast<float*>(ws + p.off_ws);
   const bool mfma = p.mfma && aligned16(x) && aligned16(dx_out);
   uint16_t* gb = mfma ? reinterpret_cast<uint16_t*>(ws + p.off_gb) : nullptr;
+  int nchunk = p.nchunk;
+  if (mfma && p.stream) {
+    // streaming form: dL/dlogits is formed inside the dx / dwg kernel, per chunk
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const uint16_t* wb = static_cast<const uint16_t*>(wg);
+    uint16_t* dxb = static_cast<uint16_t*>(dx_out);
+#define MOE_DXDWS(NTEv)                                                                                          \
+  launch_dxdw_stream<NTEv>(s, xb, wb, logits, idx, grad_w, gw_dtype, cnt, grad_aux, grad_z, aux_coef, z_coef,    \
+                           (int)N, (int)H, (int)E, (int)K, p.tc_len, p.nchunk, dxb, wsdw)
+    if (p.NTE == 1) MOE_DXDWS(1);
+    else MOE_DXDWS(2);
+#undef MOE_DXDWS
+    if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+    launch_reduce(s, wsdw, nchunk, H * E, dwg_out, wg_dtype);
+    return check_launch("moe_router_bwd");
+  }
   {
     const int ekp = p.EK * 32;
     const int rb = (int)(x_dtype == MOE_BF16);
@@ -1570,15 +1626,7 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
 #undef MOE_GLOG
   }
   if (int rc = check_launch("k_router_glogits")) return rc;
-  int nchunk = p.nchunk;
-  if (mfma && p.stream) {
-    const uint16_t* xb = static_cast<const uint16_t*>(x);
-    const uint16_t* wb = static_cast<const uint16_t*>(wg);
-    uint16_t* dxb = static_cast<uint16_t*>(dx_out);
-    if (p.NTE == 1) launch_dxdw_stream<1>(s, xb, wb, gb, (int)N, (int)H, (int)E, p.tc_len, p.nchunk, dxb, wsdw);
-    else launch_dxdw_stream<2>(s, xb, wb, gb, (int)N, (int)H, (int)E, p.tc_len, p.nchunk, dxb, wsdw);
-    if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
-  } else if (mfma) {
+  if (mfma) {
     const dim3 grid(p.nchunk, cdiv(H, 256));
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     const uint16_t* wb = static_cast<const uint16_t*>(wg);
