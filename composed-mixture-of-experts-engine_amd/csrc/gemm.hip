@@ -210,8 +210,15 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     if (slot >= chunk || L >= total) return;
     e = L / (Tm * Tn);
     const int r = L - e * Tm * Tn;
-    const int mt = r / Tn;
-    nt = r - mt * Tn;
+    // groups of (up to) 4 m-tiles, n walked within a group: the 32 tiles an XCD runs at once form a
+    // 4 x 8 block that shares 12 operand panels per k slice (an n-fastest row of 32 tiles would need 33)
+    constexpr int GM = 4;
+    const int grp = r / (GM * Tn);
+    const int m0 = grp * GM;
+    const int gm = min(Tm - m0, GM);
+    const int rr = r - grp * GM * Tn;
+    const int mt = m0 + rr % gm;
+    nt = rr / gm;
 
     mbase = mt * GBM;
     mlen = min(GBM, g.M - mbase);
