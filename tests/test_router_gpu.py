@@ -179,3 +179,23 @@ def test_router_empty_batch():
     w = torch.randn(64, 8, device=d).to(torch.bfloat16)
     idx, wt, logits, lse, cnt, stats = ops.router_forward(x, w, 2)
     assert idx.shape == (0, 2) and int(cnt.sum()) == 0
+
+
+def test_router_forward_workspace_reuse_across_paths():
+    """The streaming forward folds its finalize into the last block through a completion counter kept in the
+    reused (per stream) workspace.  Alternate shapes that take the streaming path, the packed-gate path and
+    the generic path on one stream, twice, and check every call's counts and statistics: a counter that a call
+    leaves non-zero, or that another path overwrites, shows up as missing or stale statistics."""
+    say("[router workspace reuse]")
+    seq = [
+        (16384, 4096, 8, 2, torch.bfloat16, torch.bfloat16),  # streaming, 256 blocks
+        (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # packed-gate kernel + finalize launch
+        (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),   # streaming, other block count
+        (4096, 512, 8, 2, torch.float32, torch.float32),      # generic path
+        (37, 512, 32, 1, torch.bfloat16, torch.bfloat16),     # streaming, a single block
+    ]
+    for rep in range(2):
+        for i, shape in enumerate(seq):
+            N, H, E, K, xd, wd = shape
+            x, w, _ = _inputs(N, H, E, K, xd, wd, seed=100 + 7 * i + rep)
+            _check_forward(x, w, K)
