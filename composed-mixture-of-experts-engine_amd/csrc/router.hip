@@ -1474,6 +1474,33 @@ extern "C" size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int6
   return std::max(plan_fwd(N, H, E, x_dtype, wg_dtype).total, plan_fwd(N, H, E, x_dtype, wg_dtype, false).total);
 }
 
+extern "C" int64_t moe_router_fwd_lds_bytes(int64_t N, int64_t H, int64_t E, int x_dtype, int wg_dtype) {
+  if (N <= 0 || H <= 0 || E < 1 || E > kMaxE) return 0;
+  const FwdPlan p = plan_fwd(N, H, E, x_dtype, wg_dtype);
+  const void* f = nullptr;
+  if (p.stream) {
+    if (p.NT == 1) f = p.TG == 4 ? (const void*)k_router_fwd_stream<1, 4> : p.TG == 2 ? (const void*)k_router_fwd_stream<1, 2>
+                                                                                    : (const void*)k_router_fwd_stream<1, 1>;
+    else f = p.TG == 4 ? (const void*)k_router_fwd_stream<2, 4> : p.TG == 2 ? (const void*)k_router_fwd_stream<2, 2>
+                                                                           : (const void*)k_router_fwd_stream<2, 1>;
+  } else if (p.mfma) {
+    switch (p.NT) {
+      case 1: f = (const void*)k_router_fwd_bf16<1, fwd_hs(1), fwd_u(1)>; break;
+      case 2: f = (const void*)k_router_fwd_bf16<2, fwd_hs(2), fwd_u(2)>; break;
+      case 4: f = (const void*)k_router_fwd_bf16<4, fwd_hs(4), fwd_u(4)>; break;
+      default: f = (const void*)k_router_fwd_bf16<8, fwd_hs(8), fwd_u(8)>; break;
+    }
+  } else {
+    f = (const void*)k_route_from_logits;
+  }
+  hipFuncAttributes attr{};
+  if (hipFuncGetAttributes(&attr, f) != hipSuccess) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  return (int64_t)attr.sharedSizeBytes;
+}
+
 extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias, int64_t N,
                               int64_t H, int64_t E, int64_t K, int64_t* idx_out, void* w_out, int w_dtype,
                               float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out,

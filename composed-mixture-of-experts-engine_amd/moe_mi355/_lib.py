@@ -33,6 +33,7 @@ _SIGNATURES = {
     "moe_prof_summary": (_I32, [ctypes.c_char_p, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "moe_prof_kernel_name": (_I32, [_I64, ctypes.c_char_p, _SZ]),
     "moe_router_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
+    "moe_router_fwd_lds_bytes": (_I64, [_I64, _I64, _I64, _I32, _I32]),
     "moe_router_fwd": (
         _I32,
         [_P, _I32, _P, _I32, _P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _P, _P, _F32, _F32, _P, _P, _P, _SZ,

@@ -88,6 +88,10 @@ int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
  * it); calls that share a workspace must not overlap.
  * ---------------------------------------------------------------------- */
 size_t moe_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
+/* LDS bytes per workgroup of the forward kernel a call with these sizes and dtypes launches (-1 if the runtime
+ * cannot report it): the figure MoERouter reports as RouterProfile.sram_bytes_per_block, in place of the Triton
+ * tile estimate sram_bytes = 64 * BLOCK_E * dsize * 3 (pkg/kernels/moe_router.py L:380). */
+int64_t moe_router_fwd_lds_bytes(int64_t N, int64_t H, int64_t E, int x_dtype, int wg_dtype);
 int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* bias,
                    int64_t N, int64_t H, int64_t E, int64_t K,
                    int64_t* idx_out, void* w_out, int w_dtype,
