@@ -227,132 +227,281 @@ __device__ __forceinline__ void st<uint16_t>(uint16_t* p, int64_t i, float v) {
   p[i] = f2bf(v);
 }
 
-// 8 consecutive elements <-> float[8]
+// Streaming store of an 8-element row chunk (rows written once).
 template <typename T>
-struct Vec8;
+__device__ __forceinline__ void store8_nt(T* p, const float (&f)[8]);
 template <>
-struct Vec8<uint16_t> {
-  static __device__ __forceinline__ void load(const uint16_t* p, float (&f)[8]) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+__device__ __forceinline__ void store8_nt<uint16_t>(uint16_t* p, const float (&f)[8]) {
+  u32x4 v;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f[2 * j] = __uint_as_float(v[j] << 16);
-      f[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
-    }
-  }
-  static __device__ __forceinline__ void store(uint16_t* p, const float (&f)[8]) {
-    u32x4 v;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = pack2bf(f[2 * j], f[2 * j + 1]);
-    *reinterpret_cast<u32x4*>(p) = v;
-  }
-};
+  for (int j = 0; j < 4; ++j) v[j] = pack2bf(f[2 * j], f[2 * j + 1]);
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
 template <>
-struct Vec8<float> {
-  static __device__ __forceinline__ void load(const float* p, float (&f)[8]) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f[j] = a[j];
-      f[4 + j] = b[j];
-    }
-  }
-  static __device__ __forceinline__ void store(float* p, const float (&f)[8]) {
-    *reinterpret_cast<f32x4*>(p) = f32x4{f[0], f[1], f[2], f[3]};
-    *reinterpret_cast<f32x4*>(p + 4) = f32x4{f[4], f[5], f[6], f[7]};
-  }
-};
-
-__device__ __forceinline__ bool row_live(int row, const int* __restrict__ offsets, int E) {
-  return row >= 0 && row < offsets[E];
+__device__ __forceinline__ void store8_nt<float>(float* p, const float (&f)[8]) {
+  __builtin_nontemporal_store(f32x4{f[0], f[1], f[2], f[3]}, reinterpret_cast<f32x4*>(p));
+  __builtin_nontemporal_store(f32x4{f[4], f[5], f[6], f[7]}, reinterpret_cast<f32x4*>(p + 4));
 }
 
+// 16-byte loads through a buffer descriptor that covers one row: a descriptor with no records (a slot
+// without a row) or an offset past the row's end reads zeros without touching memory.  A batch of slot
+// loads therefore needs no branch between them, and so no wait for one load before the next issues.
+typedef __amdgpu_buffer_rsrc_t row_rsrc_t;
+__device__ __forceinline__ row_rsrc_t row_rsrc(const void* row, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, nbytes, 0x00020000);
+}
+constexpr int kStreamPolicy = 2;  // nt: the rows are read once
+template <typename T>
+__device__ __forceinline__ void load8_row(row_rsrc_t r, int h0, float (&f)[8]);
+template <>
+__device__ __forceinline__ void load8_row<uint16_t>(row_rsrc_t r, int h0, float (&f)[8]) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, h0 * 2, 0, kStreamPolicy));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = __uint_as_float(v[j] << 16);
+    f[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void load8_row<float>(row_rsrc_t r, int h0, float (&f)[8]) {
+  const u32x4 a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, h0 * 4, 0, kStreamPolicy));
+  const u32x4 b = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, h0 * 4 + 16, 0, kStreamPolicy));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = __uint_as_float(a[j]);
+    f[4 + j] = __uint_as_float(b[j]);
+  }
+}
+
+// Slot metadata of one token, one slot per lane: lane l describes slot s0 + l (l < n) -- the
+// expert-output row it maps to (-1 when the slot has no computed row: dropped from the plan or
+// past offsets[E]), whether the capacity rule dropped it, and its combine weight.  The combine
+// loops read a slot's fields from its lane with readlane (wave-uniform values), so every row
+// load of a token is addressed without waiting for another load.
+struct SlotMeta {
+  int row;
+  int dropped;
+  float w;
+};
+template <typename TW>
+__device__ __forceinline__ float ld_slot_w(row_rsrc_t r, int lane);
+template <>
+__device__ __forceinline__ float ld_slot_w<float>(row_rsrc_t r, int lane) {
+  return __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, lane * 4, 0, 0));
+}
+template <>
+__device__ __forceinline__ float ld_slot_w<uint16_t>(row_rsrc_t r, int lane) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, lane * 2, 0, 0) << 16);
+}
+// The three fields are independent buffer loads (absent arrays: descriptors without records), so
+// they share one memory round trip.
+template <typename TW>
+__device__ __forceinline__ SlotMeta slot_meta(const TW* __restrict__ w, const uint8_t* __restrict__ drop,
+                                              const int* __restrict__ slot_row, int live_rows, int64_t s0, int n,
+                                              int lane) {
+  const int r = __builtin_amdgcn_raw_buffer_load_b32(row_rsrc(slot_row + s0, n * 4), lane * 4, 0, 0);
+  const int d = __builtin_amdgcn_raw_buffer_load_b8(row_rsrc(drop ? drop + s0 : nullptr, drop ? n : 0), lane, 0, 0);
+  const float wt = ld_slot_w<TW>(row_rsrc(w ? w + s0 : nullptr, w ? n * (int)sizeof(TW) : 0), lane);
+  SlotMeta m;
+  m.row = (lane < n && r >= 0 && r < live_rows) ? r : -1;
+  m.dropped = d != 0;
+  m.w = wt;
+  return m;
+}
+__device__ __forceinline__ int lane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// The wave's index in its block as a wave-uniform (scalar) value: the token a wave works on then is
+// too, and so are the buffer descriptors built from it.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// Slot batching: KG slots (2, 4 or 8: the smallest that covers min(K, 8)) are taken together and
+// U = 8 / KG of the lane's 8-element row chunks (512 columns apart) per round, so each round issues
+// about 8 independent row loads whatever K is.
+template <int KG>
+struct SlotBatch {
+  static constexpr int U = 8 / KG;
+  static constexpr int SPAN = 512 * U;  // columns one round covers
+};
+
 // ---------------------------------------------------------------------------
-// Combine: out[t, :] = sum_k w'[t,k] y[slot_row[t*K+k], :], w' = 0 for dropped
-// slots and for rows that were not computed.  One wave per token, fp32 sums.
+// Combine: out[t, :] = sum_k w[t,k] y[slot_row[t*K+k], :] over the slots that have a computed,
+// undropped row (the others contribute nothing).  One wave per token; every row load of a round is
+// issued before any is summed.  fp32 sums in slot order, one rounding at the store.
 // ---------------------------------------------------------------------------
-template <typename T, typename TW>
+template <typename T, typename TW, int KG>
 __global__ __launch_bounds__(256) void k_combine(const T* __restrict__ y, const TW* __restrict__ w,
                                                  const uint8_t* __restrict__ drop, const int* __restrict__ slot_row,
                                                  const int* __restrict__ offsets, int E, int N, int K, int H,
                                                  T* __restrict__ out) {
+  constexpr int U = SlotBatch<KG>::U;
   const int lane = threadIdx.x & 63;
-  for (int t = blockIdx.x * 4 + (threadIdx.x >> 6); t < N; t += gridDim.x * 4) {
-    for (int h0 = lane * 8; h0 < H; h0 += 512) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int k = 0; k < K; ++k) {
-        const int64_t s = (int64_t)t * K + k;
-        const int row = slot_row[s];
-        if (!row_live(row, offsets, E) || (drop && drop[s])) continue;
-        const float wk = ld<TW>(w, s);
-        float v[8];
-        Vec8<T>::load(y + (int64_t)row * H + h0, v);
+  const int live_rows = offsets[E];
+  const int rbytes = H * (int)sizeof(T);
+  for (int t = blockIdx.x * 4 + wave_id(); t < N; t += gridDim.x * 4) {
+    const int64_t s0 = (int64_t)t * K;
+    SlotMeta m = slot_meta(w, drop, slot_row, live_rows, s0, min(K, 64), lane);
+    for (int hb = 0; hb < H; hb += SlotBatch<KG>::SPAN) {
+      float acc[U][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = fmaf(wk, v[j], acc[j]);
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[u][i] = 0.f;
+      for (int kw = 0; kw < K; kw += 64) {
+        if (kw > 0) m = slot_meta(w, drop, slot_row, live_rows, s0 + kw, min(K - kw, 64), lane);
+        const int kn = min(K - kw, 64);
+        for (int kg = 0; kg < kn; kg += KG) {
+          int rk[KG];
+          float v[KG][U][8];
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            rk[j] = kg + j < kn ? lane_i(m.dropped ? -1 : m.row, kg + j) : -1;
+            const row_rsrc_t r = row_rsrc(y + (int64_t)max(rk[j], 0) * H, rk[j] >= 0 ? rbytes : 0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) load8_row<T>(r, hb + 512 * u + lane * 8, v[j][u]);
+          }
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            if (rk[j] < 0) continue;
+            const float wk = lane_f(m.w, kg + j);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) acc[u][i] = fmaf(wk, v[j][u][i], acc[u][i]);
+          }
+        }
       }
-      Vec8<T>::store(out + (int64_t)t * H + h0, acc);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int h0 = hb + 512 * u + lane * 8;
+        if (h0 < H) store8_nt<T>(out + (int64_t)t * H + h0, acc[u]);
+      }
     }
   }
 }
 
-// Combine backward: dy[row, :] = w'[t,k] dout[t, :]; dw[t,k] = <dout[t], y[row]> (0 when dropped / not live).
-template <typename T, typename TW>
+// Combine backward: dy[row, :] = w'[t,k] dout[t, :] with w' = 0 for dropped slots, and
+// dw[t,k] = <dout[t], y[row]> (0 when dropped); slots without a computed row write no dy and
+// dw = 0.  Per batch of KG slots, dout's chunks are loaded once per round together with the
+// batch's row chunks; the KG dot products reduce across the wave once the row is done.
+template <typename T, typename TW, int KG>
 __global__ __launch_bounds__(256) void k_combine_bwd(const T* __restrict__ dout, const T* __restrict__ y,
                                                      const TW* __restrict__ w, const uint8_t* __restrict__ drop,
                                                      const int* __restrict__ slot_row,
                                                      const int* __restrict__ offsets, int E, int N, int K, int H,
                                                      T* __restrict__ dy, TW* __restrict__ dw) {
+  constexpr int U = SlotBatch<KG>::U;
   const int lane = threadIdx.x & 63;
-  for (int t = blockIdx.x * 4 + (threadIdx.x >> 6); t < N; t += gridDim.x * 4) {
-    for (int k = 0; k < K; ++k) {
-      const int64_t s = (int64_t)t * K + k;
-      const int row = slot_row[s];
-      const bool live = row_live(row, offsets, E);
-      const bool dropped = drop && drop[s];
-      if (!live) {
-        if (lane == 0 && dw) st<TW>(dw, s, 0.f);
-        continue;
-      }
-      const float wk = dropped ? 0.f : ld<TW>(w, s);
-      float dot = 0.f;
-      for (int h0 = lane * 8; h0 < H; h0 += 512) {
-        float g[8], v[8], o[8];
-        Vec8<T>::load(dout + (int64_t)t * H + h0, g);
-        Vec8<T>::load(y + (int64_t)row * H + h0, v);
+  const int live_rows = offsets[E];
+  const int rbytes = H * (int)sizeof(T);
+  for (int t = blockIdx.x * 4 + wave_id(); t < N; t += gridDim.x * 4) {
+    const row_rsrc_t drow = row_rsrc(dout + (int64_t)t * H, rbytes);
+    for (int kw = 0; kw < K; kw += 64) {
+      const int kn = min(K - kw, 64);
+      const SlotMeta m = slot_meta(w, drop, slot_row, live_rows, (int64_t)t * K + kw, kn, lane);
+      float mine = 0.f;  // lane l ends with dw of slot kw + l
+      for (int kg = 0; kg < kn; kg += KG) {
+        int rk[KG];
+        float wk[KG], dot[KG];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          dot = fmaf(g[j], v[j], dot);
-          o[j] = wk * g[j];
+        for (int j = 0; j < KG; ++j) {
+          rk[j] = kg + j < kn ? lane_i(m.row, kg + j) : -1;
+          wk[j] = lane_i(m.dropped, kg + j) ? 0.f : lane_f(m.w, kg + j);
+          dot[j] = 0.f;
         }
-        Vec8<T>::store(dy + (int64_t)row * H + h0, o);
+        for (int hb = 0; hb < H; hb += SlotBatch<KG>::SPAN) {
+          float g[U][8], v[KG][U][8];
+#pragma unroll
+          for (int u = 0; u < U; ++u) load8_row<T>(drow, hb + 512 * u + lane * 8, g[u]);
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            const row_rsrc_t r = row_rsrc(y + (int64_t)max(rk[j], 0) * H, rk[j] >= 0 ? rbytes : 0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) load8_row<T>(r, hb + 512 * u + lane * 8, v[j][u]);
+          }
+          // dy needs only dout: its stores go out before the dot products wait for the rows
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            if (rk[j] < 0) continue;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+              const int h0 = hb + 512 * u + lane * 8;
+              float o[8];
+#pragma unroll
+              for (int i = 0; i < 8; ++i) o[i] = wk[j] * g[u][i];
+              if (h0 < H) store8_nt<T>(dy + (int64_t)rk[j] * H + h0, o);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            if (rk[j] < 0) continue;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) dot[j] = fmaf(g[u][i], v[j][u][i], dot[j]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < KG; ++j) {
+          if (rk[j] < 0) continue;
+          const float d = wave_sum(dot[j]);
+          if (lane == kg + j) mine = d;
+        }
       }
-      dot = wave_sum(dot);
-      if (lane == 0 && dw) st<TW>(dw, s, dropped ? 0.f : dot);
+      if (lane < kn && dw) st<TW>(dw, (int64_t)t * K + kw + lane, (m.row >= 0 && !m.dropped) ? mine : 0.f);
     }
   }
 }
 
-// Permute backward: dx[t, :] = addend[t, :] + sum_k dxp[slot_row[t*K+k], :] over live rows.
-template <typename T>
+// Permute backward: dx[t, :] = addend[t, :] + sum_k dxp[slot_row[t*K+k], :] over the slots with a
+// computed row (dropped slots have none).  Same slot batching as the combine.
+template <typename T, int KG>
 __global__ __launch_bounds__(256) void k_unpermute_sum(const T* __restrict__ dxp, const T* __restrict__ addend,
                                                        const int* __restrict__ slot_row,
                                                        const int* __restrict__ offsets, int E, int N, int K, int H,
                                                        T* __restrict__ dx) {
+  constexpr int U = SlotBatch<KG>::U;
   const int lane = threadIdx.x & 63;
-  for (int t = blockIdx.x * 4 + (threadIdx.x >> 6); t < N; t += gridDim.x * 4) {
-    for (int h0 = lane * 8; h0 < H; h0 += 512) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (addend) Vec8<T>::load(addend + (int64_t)t * H + h0, acc);
-      for (int k = 0; k < K; ++k) {
-        const int row = slot_row[(int64_t)t * K + k];
-        if (!row_live(row, offsets, E)) continue;
-        float v[8];
-        Vec8<T>::load(dxp + (int64_t)row * H + h0, v);
+  const int live_rows = offsets[E];
+  const int rbytes = H * (int)sizeof(T);
+  for (int t = blockIdx.x * 4 + wave_id(); t < N; t += gridDim.x * 4) {
+    const int64_t s0 = (int64_t)t * K;
+    SlotMeta m = slot_meta<float>(nullptr, nullptr, slot_row, live_rows, s0, min(K, 64), lane);
+    const row_rsrc_t arow = row_rsrc(addend ? addend + (int64_t)t * H : dxp, addend ? rbytes : 0);
+    for (int hb = 0; hb < H; hb += SlotBatch<KG>::SPAN) {
+      float acc[U][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += v[j];
+      for (int u = 0; u < U; ++u) load8_row<T>(arow, hb + 512 * u + lane * 8, acc[u]);  // zeros without an addend
+      for (int kw = 0; kw < K; kw += 64) {
+        if (kw > 0) m = slot_meta<float>(nullptr, nullptr, slot_row, live_rows, s0 + kw, min(K - kw, 64), lane);
+        const int kn = min(K - kw, 64);
+        for (int kg = 0; kg < kn; kg += KG) {
+          int rk[KG];
+          float v[KG][U][8];
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            rk[j] = kg + j < kn ? lane_i(m.row, kg + j) : -1;
+            const row_rsrc_t r = row_rsrc(dxp + (int64_t)max(rk[j], 0) * H, rk[j] >= 0 ? rbytes : 0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) load8_row<T>(r, hb + 512 * u + lane * 8, v[j][u]);
+          }
+#pragma unroll
+          for (int j = 0; j < KG; ++j) {
+            if (rk[j] < 0) continue;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) acc[u][i] += v[j][u][i];
+          }
+        }
       }
-      Vec8<T>::store(dx + (int64_t)t * H + h0, acc);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int h0 = hb + 512 * u + lane * 8;
+        if (h0 < H) store8_nt<T>(dx + (int64_t)t * H + h0, acc[u]);
+      }
     }
   }
 }
@@ -479,6 +628,14 @@ extern "C" int moe_permute(const void* x, int64_t row_bytes, const int32_t* row_
   return check_launch("moe_permute");
 }
 
+// Slot batch of the combine kernels: the smallest of 2, 4, 8 that covers min(K, 8).
+#define MOE_KG(k, KERNEL_CALL)                                   \
+  do {                                                           \
+    if ((k) <= 2) { constexpr int KG = 2; KERNEL_CALL; }         \
+    else if ((k) <= 4) { constexpr int KG = 4; KERNEL_CALL; }    \
+    else { constexpr int KG = 8; KERNEL_CALL; }                  \
+  } while (0)
+
 #define MOE_DT2(dt, dtw, KERNEL_CALL)                                              \
   do {                                                                            \
     if (dt == MOE_BF16 && dtw == MOE_BF16) { using T = uint16_t; using TW = uint16_t; KERNEL_CALL; } \
@@ -498,10 +655,10 @@ extern "C" int moe_combine(const void* y, int dtype, const void* w, int w_dtype,
     return fail_arg("moe_combine: null or misaligned pointer");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const unsigned nb = (unsigned)std::min<int64_t>(8192, (N + 3) / 4);
-  MOE_DT2(dtype, w_dtype,
-          MOE_LAUNCH("k_combine", (k_combine<T, TW>), dim3(nb), dim3(256), 0, s, static_cast<const T*>(y),
+  MOE_DT2(dtype, w_dtype, MOE_KG(K,
+          MOE_LAUNCH("k_combine", (k_combine<T, TW, KG>), dim3(nb), dim3(256), 0, s, static_cast<const T*>(y),
                      static_cast<const TW*>(w), drop, slot_row, offsets, (int)E, (int)N, (int)K, (int)H,
-                     static_cast<T*>(out)));
+                     static_cast<T*>(out))));
   return check_launch("moe_combine");
 }
 
@@ -517,10 +674,10 @@ extern "C" int moe_combine_bwd(const void* dout, const void* y, int dtype, const
     return fail_arg("moe_combine_bwd: null or misaligned pointer");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const unsigned nb = (unsigned)std::min<int64_t>(8192, (N + 3) / 4);
-  MOE_DT2(dtype, w_dtype,
-          MOE_LAUNCH("k_combine_bwd", (k_combine_bwd<T, TW>), dim3(nb), dim3(256), 0, s, static_cast<const T*>(dout),
+  MOE_DT2(dtype, w_dtype, MOE_KG(K,
+          MOE_LAUNCH("k_combine_bwd", (k_combine_bwd<T, TW, KG>), dim3(nb), dim3(256), 0, s, static_cast<const T*>(dout),
                      static_cast<const T*>(y), static_cast<const TW*>(w), drop, slot_row, offsets, (int)E, (int)N,
-                     (int)K, (int)H, static_cast<T*>(dy), static_cast<TW*>(dw)));
+                     (int)K, (int)H, static_cast<T*>(dy), static_cast<TW*>(dw))));
   return check_launch("moe_combine_bwd");
 }
 
@@ -536,12 +693,12 @@ extern "C" int moe_unpermute_sum(const void* dxp, const void* addend, int dtype,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const unsigned nb = (unsigned)std::min<int64_t>(8192, (N + 3) / 4);
   if (dtype == MOE_BF16)
-    MOE_LAUNCH("k_unpermute_sum", k_unpermute_sum<uint16_t>, dim3(nb), dim3(256), 0, s,
-               static_cast<const uint16_t*>(dxp), static_cast<const uint16_t*>(addend), slot_row, offsets, (int)E,
-               (int)N, (int)K, (int)H, static_cast<uint16_t*>(dx));
+    MOE_KG(K, MOE_LAUNCH("k_unpermute_sum", (k_unpermute_sum<uint16_t, KG>), dim3(nb), dim3(256), 0, s,
+                         static_cast<const uint16_t*>(dxp), static_cast<const uint16_t*>(addend), slot_row, offsets,
+                         (int)E, (int)N, (int)K, (int)H, static_cast<uint16_t*>(dx)));
   else
-    MOE_LAUNCH("k_unpermute_sum", k_unpermute_sum<float>, dim3(nb), dim3(256), 0, s, static_cast<const float*>(dxp),
-               static_cast<const float*>(addend), slot_row, offsets, (int)E, (int)N, (int)K, (int)H,
-               static_cast<float*>(dx));
+    MOE_KG(K, MOE_LAUNCH("k_unpermute_sum", (k_unpermute_sum<float, KG>), dim3(nb), dim3(256), 0, s,
+                         static_cast<const float*>(dxp), static_cast<const float*>(addend), slot_row, offsets, (int)E,
+                         (int)N, (int)K, (int)H, static_cast<float*>(dx)));
   return check_launch("moe_unpermute_sum");
 }

@@ -321,7 +321,7 @@ __device__ __forceinline__ T ld_part(const T* p) {
 // ---------------------------------------------------------------------------
 // LDS scratch the finalize needs (floats).
 template <int NTHR>
-constexpr int finalize_scratch_floats() { return 2 * kMaxE + 2 * (NTHR / 64); }
+constexpr int finalize_scratch_floats() { return 2 * kMaxE + 2 * (NTHR / 64) + 2 * NTHR; }
 
 template <int NTHR, bool COH = false>
 __device__ __forceinline__ void router_finalize_block(const int* __restrict__ part_cnt, const float* __restrict__ part_p,
@@ -332,26 +332,28 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
   float* s_c = scratch;                                                       // [kMaxE]
   float* s_pe = scratch + kMaxE;                                              // [kMaxE]
   float(*s_red)[NTHR / 64] = reinterpret_cast<float(*)[NTHR / 64]>(scratch + 2 * kMaxE);  // [2][NTHR/64]
+  int* s_pc = reinterpret_cast<int*>(scratch + 2 * kMaxE + 2 * (NTHR / 64));  // [NTHR]
+  float* s_pp = scratch + 2 * kMaxE + 2 * (NTHR / 64) + NTHR;                 // [NTHR]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  // threads per expert: a power of two <= 64 so each expert's threads sit in one wave
-  int tpe = 1;
-  while (tpe * 2 <= 64 && tpe * 2 * E <= NTHR) tpe *= 2;
-  const int epp = NTHR / tpe;  // experts per pass
-  for (int e0 = 0; e0 < E; e0 += epp) {
-    const int e = e0 + tid / tpe;
-    const int j = tid % tpe;
+  // Per-expert sums over the blocks: thread (jj, e) = (tid / E, tid % E) sums blocks jj, jj + nj, ...
+  // (experts fastest across lanes, so one load instruction reads consecutive experts of a block),
+  // then thread e folds the nj partial sums in jj order.
+  {
+    const int nj = NTHR / E;  // E <= kMaxE <= NTHR
+    const int e = tid % E;
+    const int jj = tid / E;
     int c = 0;
     float p = 0.f;
-    if (e < E) {
-      int b = j;
-      for (; b + 7 * tpe < nblk; b += 8 * tpe) {  // 8 independent loads in flight
+    if (jj < nj) {
+      int b = jj;
+      for (; b + 7 * nj < nblk; b += 8 * nj) {  // 8 independent loads in flight
         int cv[8];
         float pv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          cv[u] = ld_part<COH>(&part_cnt[(int64_t)(b + u * tpe) * E + e]);
-          pv[u] = ld_part<COH>(&part_p[(int64_t)(b + u * tpe) * E + e]);
+          cv[u] = ld_part<COH>(&part_cnt[(int64_t)(b + u * nj) * E + e]);
+          pv[u] = ld_part<COH>(&part_p[(int64_t)(b + u * nj) * E + e]);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -359,20 +361,25 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
           p += pv[u];
         }
       }
-      for (; b < nblk; b += tpe) {
+      for (; b < nblk; b += nj) {
         c += ld_part<COH>(&part_cnt[(int64_t)b * E + e]);
         p += ld_part<COH>(&part_p[(int64_t)b * E + e]);
       }
     }
-    for (int o = tpe / 2; o > 0; o >>= 1) {
-      c += __shfl_xor(c, o);
-      p += __shfl_xor(p, o);
-    }
-    if (j == 0 && e < E) {
-      cnt_out[e] = c;
-      s_c[e] = (float)c;
-      s_pe[e] = p / (float)N;
-      stats[MOE_STATS_HEAD + e] = p / (float)N;
+    s_pc[tid] = c;
+    s_pp[tid] = p;
+    __syncthreads();
+    if (tid < E) {
+      c = s_pc[tid];
+      p = s_pp[tid];
+      for (int q = 1; q < nj; ++q) {
+        c += s_pc[q * E + tid];
+        p += s_pp[q * E + tid];
+      }
+      cnt_out[tid] = c;
+      s_c[tid] = (float)c;
+      s_pe[tid] = p / (float)N;
+      stats[MOE_STATS_HEAD + tid] = p / (float)N;
     }
   }
   float z = 0.f, nf = 0.f;
@@ -435,14 +442,16 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
   }
 }
 
-__global__ __launch_bounds__(256) void k_router_finalize(const int* __restrict__ part_cnt,
+// Standalone finalize: one block; 1024 threads give each expert up to 16 loaders of its partials.
+constexpr int kFinThreads = 1024;
+__global__ __launch_bounds__(kFinThreads) void k_router_finalize(const int* __restrict__ part_cnt,
                                                          const float* __restrict__ part_p,
                                                          const float* __restrict__ part_z, int nblk, int N, int E,
                                                          int K, float aux_coef, float z_coef,
                                                          int64_t* __restrict__ cnt_out, float* __restrict__ stats,
                                                          float* __restrict__ aux_out, float* __restrict__ z_out) {
-  __shared__ float scratch[finalize_scratch_floats<256>()];
-  router_finalize_block<256>(part_cnt, part_p, part_z, nblk, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out, z_out,
+  __shared__ float scratch[finalize_scratch_floats<kFinThreads>()];
+  router_finalize_block<kFinThreads>(part_cnt, part_p, part_z, nblk, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out, z_out,
                              scratch);
 }
 
@@ -1562,7 +1571,7 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
       default: return fail_arg("moe_router_fwd: internal tile error");
     }
     if (int rc = check_launch("k_router_fwd_bf16")) return rc;
-    MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(256), 0, s, pc, pp, pz, p.nblk, (int)N, (int)E, (int)K,
+    MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(kFinThreads), 0, s, pc, pp, pz, p.nblk, (int)N, (int)E, (int)K,
                        aux_coef, z_coef, cnt_out, stats_out, aux_out, z_out);
   } else {
     FwdPlan pg = p;
@@ -1580,7 +1589,7 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
     const int nblk = cdiv(N, tpb);
     MOE_LAUNCH("k_route_from_logits", k_route_from_logits, dim3(nblk), dim3(256), 0, s, logits_out, (int)N, (int)E, (int)K, tpb,
                        idx_out, w_out, w_dtype, lse_out, pc, pp, pz);
-    MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(256), 0, s, pc, pp, pz, nblk, (int)N, (int)E, (int)K,
+    MOE_LAUNCH("k_router_finalize", k_router_finalize, dim3(1), dim3(kFinThreads), 0, s, pc, pp, pz, nblk, (int)N, (int)E, (int)K,
                        aux_coef, z_coef, cnt_out, stats_out, aux_out, z_out);
   }
   return check_launch("moe_router_fwd");
