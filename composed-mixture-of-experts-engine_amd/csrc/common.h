@@ -68,6 +68,15 @@ __device__ __forceinline__ void lds_sync() {
   __asm__ volatile("" ::: "memory");
 }
 
+// Raw buffer descriptor over nbytes at base: loads at offsets past nbytes (or through a descriptor with
+// no records) return zeros without touching memory.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc_t;
+__device__ __forceinline__ buf_rsrc_t buf_rsrc(const void* base, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nbytes, 0x00020000);
+}
+// Cache-policy operand of the buffer loads: sc1 makes a load read past this XCD's L2 (agent coherence).
+constexpr int kPolicyCoherent = 16;
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
@@ -82,21 +91,75 @@ __device__ __forceinline__ T wave_max(T v) {
   return v;
 }
 
+// Cross-lane moves inside each aligned row of 16 lanes by DPP (a VALU operand modifier: no LDS traffic,
+// a few cycles of latency).  Step 0 pairs lane l with l^1 and step 1 with l^2 (quad permutes), step 2
+// with 7-l inside each half row (row_half_mirror) and step 3 with 15-l (row_mirror): combining a value
+// with its partner's at each step leaves the combination of all 16 lanes in every lane of the row, and
+// for a commutative combine every lane holds bit-identical results.
+template <int STEP>
+__device__ __forceinline__ int row16_partner(int v) {
+  constexpr int kCtrl = STEP == 0 ? 0xB1 : (STEP == 1 ? 0x4E : (STEP == 2 ? 0x141 : 0x140));
+  return __builtin_amdgcn_update_dpp(v, v, kCtrl, 0xF, 0xF, false);
+}
+template <int STEP>
+__device__ __forceinline__ float row16_partner(float v) {
+  return __int_as_float(row16_partner<STEP>(__float_as_int(v)));
+}
+
 // Reductions inside each aligned group of 16 lanes.
 __device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v += row16_partner<0>(v);
+  v += row16_partner<1>(v);
+  v += row16_partner<2>(v);
+  v += row16_partner<3>(v);
   return v;
 }
 __device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  v = fmaxf(v, row16_partner<0>(v));
+  v = fmaxf(v, row16_partner<1>(v));
+  v = fmaxf(v, row16_partner<2>(v));
+  v = fmaxf(v, row16_partner<3>(v));
   return v;
 }
 
-// Top-k ordering: larger value first; on an exact tie the lower index wins.
 __device__ __forceinline__ bool better(float v, int e, float bv, int be) {
   return v > bv || (v == bv && e < be);
+}
+
+// Order-preserving map of a float to uint32: a larger float gets a larger key (-0 is folded into +0 so
+// the two compare equal as floats do); every float's key is nonzero, so 0 can mark "no candidate".
+// NaN must be mapped to -inf by the caller.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float order_val(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Row-wide max / min of unsigned / signed 32-bit values (the DPP move folds into the max / min).
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)row16_partner<0>((int)v));
+  v = max(v, (uint32_t)row16_partner<1>((int)v));
+  v = max(v, (uint32_t)row16_partner<2>((int)v));
+  v = max(v, (uint32_t)row16_partner<3>((int)v));
+  return v;
+}
+__device__ __forceinline__ int row16_min_i32(int v) {
+  v = min(v, row16_partner<0>(v));
+  v = min(v, row16_partner<1>(v));
+  v = min(v, row16_partner<2>(v));
+  v = min(v, row16_partner<3>(v));
+  return v;
+}
+
+// Arg-max over each row of 16 lanes of (key, index): the larger key, the lower index on a tie.  Two
+// mask-free passes: the row max of the keys, then the row min of the indices of the lanes holding it.
+__device__ __forceinline__ void row16_argmax_key(uint32_t& bk, int& be) {
+  const uint32_t w = row16_max_u32(bk);
+  be = row16_min_i32(bk == w ? be : 0x7fffffff);
+  bk = w;
 }
 
 inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }

@@ -246,10 +246,8 @@ __device__ __forceinline__ void store8_nt<float>(float* p, const float (&f)[8]) 
 // 16-byte loads through a buffer descriptor that covers one row: a descriptor with no records (a slot
 // without a row) or an offset past the row's end reads zeros without touching memory.  A batch of slot
 // loads therefore needs no branch between them, and so no wait for one load before the next issues.
-typedef __amdgpu_buffer_rsrc_t row_rsrc_t;
-__device__ __forceinline__ row_rsrc_t row_rsrc(const void* row, int nbytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(row), (short)0, nbytes, 0x00020000);
-}
+typedef buf_rsrc_t row_rsrc_t;
+__device__ __forceinline__ row_rsrc_t row_rsrc(const void* row, int nbytes) { return buf_rsrc(row, nbytes); }
 constexpr int kStreamPolicy = 2;  // nt: the rows are read once
 template <typename T>
 __device__ __forceinline__ void load8_row(row_rsrc_t r, int h0, float (&f)[8]);

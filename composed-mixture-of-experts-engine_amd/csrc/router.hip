@@ -76,11 +76,14 @@ __device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int 
   for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
   float zacc = 0.f;
   int nf = 0;
+  // The row of 16 lanes g owns tokens t0 + 4g + i, i < 4; the four tokens are processed side by side
+  // (independent dependency chains for the scheduler to interleave).
+  float lg[4][NT], m[4], inv[4];
+  uint32_t kh[4][NT];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int tt = t0 + g * 4 + i;
     const bool valid = tt < N;
-    float lg[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int e = nt * 16 + n;
@@ -91,72 +94,84 @@ __device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int 
         if (!isfinite(v)) ++nf;
       }
       if (v != v) v = -INFINITY;  // NaN never wins a top-k slot
-      lg[nt] = (e < E) ? v : -INFINITY;
+      lg[i][nt] = (e < E) ? v : -INFINITY;
     }
-    float m = lg[0];
+    float mi = lg[i][0];
 #pragma unroll
-    for (int nt = 1; nt < NT; ++nt) m = fmaxf(m, lg[nt]);
-    m = row16_max(m);
+    for (int nt = 1; nt < NT; ++nt) mi = fmaxf(mi, lg[i][nt]);
+    m[i] = row16_max(mi);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tt = t0 + g * 4 + i;
+    float ex[NT];
     float s = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) s += expf(lg[nt] - m);
+    for (int nt = 0; nt < NT; ++nt) {
+      ex[nt] = expf(lg[i][nt] - m[i]);
+      s += ex[nt];
+    }
     s = row16_sum(s);
-    const float inv = 1.f / s;
-    const float lse = m + logf(s);
-    if (valid) {
+    inv[i] = 1.f / s;
+    const float lse = m[i] + logf(s);
+    if (tt < N) {
       if (n == 0) lse_out[tt] = lse;
       zacc += lse * lse;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) pacc[nt] += expf(lg[nt] - m) * inv;
+      for (int nt = 0; nt < NT; ++nt) pacc[nt] += ex[nt] * inv[i];
     }
+    // order-preserving keys of the logits (0: no candidate, an expert past E or one already taken)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) kh[i][nt] = (nt * 16 + n < E) ? order_key(lg[i][nt]) : 0u;
+  }
 
-    // top-k: K rounds of row argmax; round r's winner is kept by lane r % 16.
-    uint32_t sel = 0;
-    int e_slot0 = 0, e_slot1 = 0;
-    float p_slot0 = 0.f, p_slot1 = 0.f;
-    float psum = 0.f;
-    for (int r = 0; r < K; ++r) {
-      float bv = -INFINITY;
-      int be = 0x7fffffff;
+  // top-k: K rounds of a row arg-max over the keys; the lowest expert id wins a tie.  Round r's winner
+  // is kept by lane r % 16 and its key is cleared in the lane that holds it.  Branch-free: per round and
+  // token, a max over the lane's NT keys and four DPP exchange steps across the row.
+  int e_slot0[4], e_slot1[4];
+  float p_slot0[4], p_slot1[4], psum[4];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int e = nt * 16 + n;
-        if (e < E && !((sel >> nt) & 1u) && better(lg[nt], e, bv, be)) {
-          bv = lg[nt];
-          be = e;
-        }
-      }
+  for (int i = 0; i < 4; ++i) {
+    e_slot0[i] = e_slot1[i] = 0;
+    p_slot0[i] = p_slot1[i] = psum[i] = 0.f;
+  }
+  for (int r = 0; r < K; ++r) {
 #pragma unroll
-      for (int o = 8; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oe = __shfl_xor(be, o);
-        if (better(ov, oe, bv, be)) {
-          bv = ov;
-          be = oe;
-        }
+    for (int i = 0; i < 4; ++i) {
+      uint32_t bh = kh[i][0];
+      int bnt = 0;
+#pragma unroll
+      for (int nt = 1; nt < NT; ++nt) {  // strict '>' keeps the lower tile (lower id) on a tie
+        const bool t = kh[i][nt] > bh;
+        bh = t ? kh[i][nt] : bh;
+        bnt = t ? nt : bnt;
       }
-      if ((be & 15) == n) sel |= 1u << (be >> 4);
-      const float pv = expf(bv - m) * inv;
-      psum += pv;
-      if (r == n) {
-        e_slot0 = be;
-        p_slot0 = pv;
-      } else if (r == n + 16) {
-        e_slot1 = be;
-        p_slot1 = pv;
-      }
+      int be = bh ? bnt * 16 + n : 0x7fffffff;
+      row16_argmax_key(bh, be);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) kh[i][nt] = (be == nt * 16 + n) ? 0u : kh[i][nt];  // the winner's lane
+      const float pv = expf(order_val(bh) - m[i]) * inv[i];
+      psum[i] += pv;
+      e_slot0[i] = r == n ? be : e_slot0[i];
+      p_slot0[i] = r == n ? pv : p_slot0[i];
+      e_slot1[i] = r == n + 16 ? be : e_slot1[i];
+      p_slot1[i] = r == n + 16 ? pv : p_slot1[i];
     }
-    const float rden = 1.f / fmaxf(psum, 1e-30f);
-    if (valid) {
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tt = t0 + g * 4 + i;
+    const float rden = 1.f / fmaxf(psum[i], 1e-30f);
+    if (tt < N) {
       if (n < K) {
-        idx_out[(int64_t)tt * K + n] = e_slot0;
-        store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0 * rden);
-        atomicAdd(&s_cnt[e_slot0], 1);
+        idx_out[(int64_t)tt * K + n] = e_slot0[i];
+        store_f(w_out, w_dt, (int64_t)tt * K + n, p_slot0[i] * rden);
+        atomicAdd(&s_cnt[e_slot0[i]], 1);
       }
       if (n + 16 < K) {
-        idx_out[(int64_t)tt * K + n + 16] = e_slot1;
-        store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1 * rden);
-        atomicAdd(&s_cnt[e_slot1], 1);
+        idx_out[(int64_t)tt * K + n + 16] = e_slot1[i];
+        store_f(w_out, w_dt, (int64_t)tt * K + n + 16, p_slot1[i] * rden);
+        atomicAdd(&s_cnt[e_slot1[i]], 1);
       }
     }
   }
@@ -321,7 +336,7 @@ __device__ __forceinline__ T ld_part(const T* p) {
 // ---------------------------------------------------------------------------
 // LDS scratch the finalize needs (floats).
 template <int NTHR>
-constexpr int finalize_scratch_floats() { return 2 * kMaxE + 2 * (NTHR / 64) + 2 * NTHR; }
+constexpr int finalize_scratch_floats() { return 2 * kMaxE + 2 * (NTHR / 64) + 8 * NTHR; }
 
 template <int NTHR, bool COH = false>
 __device__ __forceinline__ void router_finalize_block(const int* __restrict__ part_cnt, const float* __restrict__ part_p,
@@ -332,54 +347,95 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
   float* s_c = scratch;                                                       // [kMaxE]
   float* s_pe = scratch + kMaxE;                                              // [kMaxE]
   float(*s_red)[NTHR / 64] = reinterpret_cast<float(*)[NTHR / 64]>(scratch + 2 * kMaxE);  // [2][NTHR/64]
-  int* s_pc = reinterpret_cast<int*>(scratch + 2 * kMaxE + 2 * (NTHR / 64));  // [NTHR]
-  float* s_pp = scratch + 2 * kMaxE + 2 * (NTHR / 64) + NTHR;                 // [NTHR]
+  int* s_pc = reinterpret_cast<int*>(scratch + 2 * kMaxE + 2 * (NTHR / 64));  // [nj][E] <= 4 * NTHR
+  float* s_pp = scratch + 2 * kMaxE + 2 * (NTHR / 64) + 4 * NTHR;             // [nj][E]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  // Per-expert sums over the blocks: thread (jj, e) = (tid / E, tid % E) sums blocks jj, jj + nj, ...
-  // (experts fastest across lanes, so one load instruction reads consecutive experts of a block),
-  // then thread e folds the nj partial sums in jj order.
+  // Per-expert sums over the blocks.  Thread (jj, q) = (tid / nq, tid % nq) owns V consecutive experts
+  // (V = 4 when E % 4 == 0: one 16-byte load per array and block) and sums blocks jj, jj + nj, ... (experts
+  // fastest across lanes, so a load instruction reads consecutive experts of one block); thread e then folds
+  // the nj partial sums in jj order.
   {
-    const int nj = NTHR / E;  // E <= kMaxE <= NTHR
-    const int e = tid % E;
-    const int jj = tid / E;
-    int c = 0;
-    float p = 0.f;
+    const bool quad = (E & 3) == 0;
+    const int V = quad ? 4 : 1;
+    const int nq = E / V;
+    const int nj = NTHR / nq;  // E <= kMaxE <= NTHR
+    const int q = tid % nq;
+    const int jj = tid / nq;
+    int c[4] = {0, 0, 0, 0};
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
     if (jj < nj) {
-      int b = jj;
-      for (; b + 7 * nj < nblk; b += 8 * nj) {  // 8 independent loads in flight
-        int cv[8];
-        float pv[8];
+      if (quad) {
+        const buf_rsrc_t rc = buf_rsrc(part_cnt, nblk * E * 4), rp = buf_rsrc(part_p, nblk * E * 4);
+        constexpr int pol = COH ? kPolicyCoherent : 0;
+        int b = jj;
+        for (; b + 3 * nj < nblk; b += 4 * nj) {  // 8 independent 16-byte loads in flight
+          u32x4 cv[4], pv[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          cv[u] = ld_part<COH>(&part_cnt[(int64_t)(b + u * nj) * E + e]);
-          pv[u] = ld_part<COH>(&part_p[(int64_t)(b + u * nj) * E + e]);
-        }
+          for (int u = 0; u < 4; ++u) {
+            const int off = ((b + u * nj) * E + 4 * q) * 4;
+            cv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, pol));
+            pv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, pol));
+          }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          c += cv[u];
-          p += pv[u];
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              c[i] += (int)cv[u][i];
+              p[i] += __uint_as_float(pv[u][i]);
+            }
         }
-      }
-      for (; b < nblk; b += nj) {
-        c += ld_part<COH>(&part_cnt[(int64_t)b * E + e]);
-        p += ld_part<COH>(&part_p[(int64_t)b * E + e]);
+        for (; b < nblk; b += nj) {
+          const int off = (b * E + 4 * q) * 4;
+          const u32x4 cv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, pol));
+          const u32x4 pv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, pol));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            c[i] += (int)cv[i];
+            p[i] += __uint_as_float(pv[i]);
+          }
+        }
+      } else {
+        int b = jj;
+        for (; b + 7 * nj < nblk; b += 8 * nj) {  // 8 independent loads in flight
+          int cv[8];
+          float pv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            cv[u] = ld_part<COH>(&part_cnt[(int64_t)(b + u * nj) * E + q]);
+            pv[u] = ld_part<COH>(&part_p[(int64_t)(b + u * nj) * E + q]);
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            c[0] += cv[u];
+            p[0] += pv[u];
+          }
+        }
+        for (; b < nblk; b += nj) {
+          c[0] += ld_part<COH>(&part_cnt[(int64_t)b * E + q]);
+          p[0] += ld_part<COH>(&part_p[(int64_t)b * E + q]);
+        }
       }
     }
-    s_pc[tid] = c;
-    s_pp[tid] = p;
+    // partial sums land in LDS at [jj][expert]
+    if (jj < nj) {
+      for (int i = 0; i < V; ++i) {
+        s_pc[jj * E + q * V + i] = c[i];
+        s_pp[jj * E + q * V + i] = p[i];
+      }
+    }
     __syncthreads();
     if (tid < E) {
-      c = s_pc[tid];
-      p = s_pp[tid];
-      for (int q = 1; q < nj; ++q) {
-        c += s_pc[q * E + tid];
-        p += s_pp[q * E + tid];
+      int cs = s_pc[tid];
+      float ps = s_pp[tid];
+      for (int j = 1; j < nj; ++j) {
+        cs += s_pc[j * E + tid];
+        ps += s_pp[j * E + tid];
       }
-      cnt_out[tid] = c;
-      s_c[tid] = (float)c;
-      s_pe[tid] = p / (float)N;
-      stats[MOE_STATS_HEAD + tid] = p / (float)N;
+      cnt_out[tid] = cs;
+      s_c[tid] = (float)cs;
+      s_pe[tid] = ps / (float)N;
+      stats[MOE_STATS_HEAD + tid] = ps / (float)N;
     }
   }
   float z = 0.f, nf = 0.f;
@@ -479,6 +535,50 @@ __device__ __forceinline__ void lds_dma16_stream(const void* src, uint32_t lds) 
 template <int N>
 __device__ __forceinline__ void router_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Block tail of the streaming forwards (512 threads): the block's partial statistics (fixed-order sums over
+// its TG token groups) go to part_* as write-through stores, and the last block to finish (ticket counter:
+// zero on entry, reset to zero by that block) folds every block's partials, so the finalize needs no launch
+// of its own.  The partials are at the coherence point before the ticket increment: every thread waits for
+// its own stores (s_waitcnt: a workgroup barrier alone does not wait for global stores) before the barrier
+// that precedes thread 0's increment, and the last block reads them past the L2.
+template <int TG, int NT>
+__device__ __forceinline__ void fwd_block_tail(const int* s_cnt, const float (*s_p)[NT * 16], const float* s_z,
+                                               const int* s_nf, int& s_last, float* s_fin, int N, int E, int K,
+                                               int* __restrict__ part_cnt, float* __restrict__ part_p,
+                                               float* __restrict__ part_z, unsigned* __restrict__ ticket,
+                                               float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
+                                               float* __restrict__ stats, float* __restrict__ aux_out,
+                                               float* __restrict__ z_out) {
+  for (int e = threadIdx.x; e < E; e += 512) {
+    float p = 0.f;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) p += s_p[q][e];
+    st_part(&part_cnt[(int64_t)blockIdx.x * E + e], s_cnt[e]);
+    st_part(&part_p[(int64_t)blockIdx.x * E + e], p);
+  }
+  if (threadIdx.x == 0) {
+    float z = 0.f;
+    int nfs = 0;
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+      z += s_z[q];
+      nfs += s_nf[q];
+    }
+    st_part(&part_z[2 * blockIdx.x], z);
+    st_part(&part_z[2 * blockIdx.x + 1], (float)nfs);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  router_finalize_block<512, true>(part_cnt, part_p, part_z, gridDim.x, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out,
+                                   z_out, s_fin);
+  if (threadIdx.x == 0) *ticket = 0u;
 }
 
 template <int NT, int TG>
@@ -613,38 +713,129 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
                     &s_z[wv], &s_nf[wv]);
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 512) {
-    float p = 0.f;
-#pragma unroll
-    for (int q = 0; q < TG; ++q) p += s_p[q][e];
-    st_part(&part_cnt[(int64_t)blockIdx.x * E + e], s_cnt[e]);
-    st_part(&part_p[(int64_t)blockIdx.x * E + e], p);
+  fwd_block_tail<TG, NT>(s_cnt, s_p, s_z, s_nf, s_last, s_fin, N, E, K, part_cnt, part_p, part_z, ticket, aux_coef,
+                         z_coef, cnt_out, stats, aux_out, z_out);
+}
+
+// ---------------------------------------------------------------------------
+// Forward, wide streaming form (bf16 x bf16, 32 < E <= 256 as NT = 4, 8 or 16 tiles of 16 experts,
+// H % 64 == 0).  With many experts the gate is as large per hidden column as a sizeable batch of token
+// rows, so the block is sized to amortise it: 128 token rows per block (8 waves, one 16-token group
+// each).  The block streams 64-column slices through a ring of kSlots LDS slots by LDS-DMA with the
+// streaming cache policy: the x tile (128 rows x 128 bytes, 16-byte units XOR-swizzled by (row >> 1) & 7,
+// so the 16 rows one fragment read touches hit distinct bank groups) and the matching two 32-row chunks
+// of the gate in MFMA fragment order (k_pack_gate's layout), which ride along as one contiguous range.
+// Each wave reads its A fragment and the NT B fragments as 16-byte LDS reads and accumulates its
+// group's logits over the whole hidden dim in registers, so the epilogue routes straight from them.
+// ---------------------------------------------------------------------------
+template <int NT>
+struct WideFwd {
+  static constexpr int ROWS = 128;
+  static constexpr int XB = ROWS * 128;  // x tile of one slice (16 KB)
+  static constexpr int GB = NT * 2048;   // packed gate of one slice: 2 chunks x NT tiles x 1 KB
+  static constexpr int SLOT = XB + GB;
+  static constexpr int XI = XB / 8192;   // x DMA instructions per wave per slice
+  static constexpr int GI = GB / 8192;   // gate DMA instructions per wave per slice
+  static constexpr int GPS = XI + GI;
+  static constexpr int kSlots = NT == 4 ? 6 : (NT == 8 ? 4 : 3);  // <= 144 KB of ring
+};
+
+template <int GPS>
+__device__ __forceinline__ void wide_wait(int ahead) {
+  // at most `ahead` later slices (GPS DMA instructions each) may still be in flight
+  switch (ahead) {
+    case 0: router_wait_vmcnt<0>(); break;
+    case 1: router_wait_vmcnt<GPS>(); break;
+    case 2: router_wait_vmcnt<2 * GPS>(); break;
+    case 3: router_wait_vmcnt<3 * GPS>(); break;
+    default: router_wait_vmcnt<4 * GPS>(); break;
   }
-  if (threadIdx.x == 0) {
-    float z = 0.f;
-    int nfs = 0;
+}
+
+template <int NT>
+__global__ __launch_bounds__(512) void k_router_fwd_wide(
+    const uint16_t* __restrict__ x, const i16x8* __restrict__ wp, const float* __restrict__ bias, int N, int H,
+    int E, int K, int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
+    float* __restrict__ lse_out, int* __restrict__ part_cnt, float* __restrict__ part_p, float* __restrict__ part_z,
+    unsigned* __restrict__ ticket, float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
+    float* __restrict__ stats, float* __restrict__ aux_out, float* __restrict__ z_out) {
+  using P = WideFwd<NT>;
+  constexpr int TG = 8;
+  static_assert(P::kSlots - 2 <= 4, "wide_wait covers at most four slices ahead");
+  constexpr int RING = P::kSlots * P::SLOT;
+  // after the stream the ring holds the epilogue's small arrays
+  constexpr int O_CNT = 0, O_P = O_CNT + NT * 16 * 4, O_Z = O_P + TG * NT * 16 * 4, O_NF = O_Z + TG * 4;
+  constexpr int O_LAST = O_NF + TG * 4, O_FIN = O_LAST + 16;
+  constexpr int EPI = O_FIN + finalize_scratch_floats<512>() * 4;
+  static_assert(RING >= EPI, "ring too small for the epilogue arrays");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING];
+  int* s_cnt = reinterpret_cast<int*>(ring + O_CNT);
+  float(*s_p)[NT * 16] = reinterpret_cast<float(*)[NT * 16]>(ring + O_P);
+  float* s_z = reinterpret_cast<float*>(ring + O_Z);
+  int* s_nf = reinterpret_cast<int*>(ring + O_NF);
+  int& s_last = *reinterpret_cast<int*>(ring + O_LAST);
+  float* s_fin = reinterpret_cast<float*>(ring + O_FIN);
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int t0 = blockIdx.x * P::ROWS;
+
+  // x DMA: instruction j (= XI*wv + q) of a slice fills rows 8j .. 8j+7; lane l writes row 8j + l/8, LDS
+  // unit l%8, which holds the row's 16-byte unit (l%8) ^ ((row >> 1) & 7) (rows past N re-read row N-1)
+  const uint16_t* xsrc[P::XI];
 #pragma unroll
-    for (int q = 0; q < TG; ++q) {
-      z += s_z[q];
-      nfs += s_nf[q];
+  for (int q = 0; q < P::XI; ++q) {
+    const int row = 8 * (P::XI * wv + q) + (lane >> 3);
+    const int u = (lane & 7) ^ ((row >> 1) & 7);
+    xsrc[q] = x + (int64_t)min(t0 + row, N - 1) * H + u * 8;
+  }
+  const uint8_t* gsrc = reinterpret_cast<const uint8_t*>(wp) + (P::GI * wv) * 1024 + lane * 16;
+  const int nsl = H >> 6;
+  auto slot_ptr = [&](int sl) { return ring + (sl % P::kSlots) * P::SLOT; };
+  auto issue = [&](int sl) {
+    uint8_t* const sp = slot_ptr(sl);
+#pragma unroll
+    for (int q = 0; q < P::XI; ++q) lds_dma16_stream(xsrc[q] + sl * 64, lds_addr_r(sp + (P::XI * wv + q) * 1024));
+#pragma unroll
+    for (int q = 0; q < P::GI; ++q)
+      lds_dma16_stream(gsrc + (int64_t)sl * P::GB + q * 1024, lds_addr_r(sp + P::XB + (P::GI * wv + q) * 1024));
+  };
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int sl = 0; sl < P::kSlots - 1; ++sl)
+    if (sl < nsl) issue(sl);
+  const int arow = 16 * wv + n;  // this lane's A row in the x tile
+  for (int sl = 0; sl < nsl; ++sl) {
+    wide_wait<P::GPS>(min(P::kSlots - 2, nsl - 1 - sl));
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's part of slice sl is in LDS; every wave is done with slice sl-1
+    __asm__ volatile("" ::: "memory");
+    if (sl + P::kSlots - 1 < nsl) issue(sl + P::kSlots - 1);  // into the slot of slice sl-1
+    const uint8_t* const sp = slot_ptr(sl);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const i16x8 a = *reinterpret_cast<const i16x8*>(sp + arow * 128 + (((4 * h + g) ^ ((arow >> 1) & 7)) << 4));
+      const i16x8* gt = reinterpret_cast<const i16x8*>(sp + P::XB) + h * NT * 64 + lane;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, gt[nt * 64]), acc[nt]);
     }
-    st_part(&part_z[2 * blockIdx.x], z);
-    st_part(&part_z[2 * blockIdx.x + 1], (float)nfs);
   }
-  // ---- the last block folds every block's partials.  The partials are write-through stores; every
-  // thread waits for its own to complete (s_waitcnt: a workgroup barrier alone does not wait for global
-  // stores), so after the barrier they are all at the coherence point before thread 0's ticket
-  // increment, and the last block reads them past the L2. ----
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // every wave is done with the ring
+
+  for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
   __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+  route_group<NT>(acc, t0 + 16 * wv, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt, s_p[wv],
+                  &s_z[wv], &s_nf[wv]);
   __syncthreads();
-  if (!s_last) return;
-  router_finalize_block<512, true>(part_cnt, part_p, part_z, gridDim.x, N, E, K, aux_coef, z_coef, cnt_out, stats, aux_out,
-                                   z_out, s_fin);
-  if (threadIdx.x == 0) *ticket = 0u;
+  fwd_block_tail<TG, NT>(s_cnt, s_p, s_z, s_nf, s_last, s_fin, N, E, K, part_cnt, part_p, part_z, ticket, aux_coef,
+                         z_coef, cnt_out, stats, aux_out, z_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -1339,6 +1530,7 @@ int fwd_tokens_per_block(int NT) { return 16 * (4 / fwd_hs(NT)); }
 struct FwdPlan {
   bool mfma;
   bool stream;  // k_router_fwd_stream (E <= 32, H % 256 == 0)
+  bool wide;    // k_router_fwd_wide (32 < E <= 256, H % 64 == 0)
   int NT, TG;
   int nblk;
   size_t off_wp, off_cnt, off_p, off_z, off_ticket, total;
@@ -1353,7 +1545,12 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt, bool allow
   if (p.NT == 3) p.NT = 4;
   if (p.NT > 4 && p.NT < 8) p.NT = 8;
   p.stream = allow_stream && p.mfma && E <= 32 && H % 256 == 0;
-  if (p.stream) {
+  p.wide = allow_stream && x_dt == MOE_BF16 && w_dt == MOE_BF16 && E > 32 && E <= kMaxE && H % 64 == 0;
+  if (p.wide) {
+    p.mfma = true;
+    p.NT = E <= 64 ? 4 : (E <= 128 ? 8 : 16);
+    p.nblk = cdiv(N, WideFwd<4>::ROWS);
+  } else if (p.stream) {
     // 16 * TG tokens per block: the largest TG that still gives one block per CU (256)
     p.TG = N >= 256 * 64 ? 4 : (N >= 256 * 32 ? 2 : 1);
     p.nblk = cdiv(N, 16 * p.TG);
@@ -1487,7 +1684,10 @@ extern "C" int64_t moe_router_fwd_lds_bytes(int64_t N, int64_t H, int64_t E, int
   if (N <= 0 || H <= 0 || E < 1 || E > kMaxE) return 0;
   const FwdPlan p = plan_fwd(N, H, E, x_dtype, wg_dtype);
   const void* f = nullptr;
-  if (p.stream) {
+  if (p.wide) {
+    f = p.NT == 4 ? (const void*)k_router_fwd_wide<4> : p.NT == 8 ? (const void*)k_router_fwd_wide<8>
+                                                                 : (const void*)k_router_fwd_wide<16>;
+  } else if (p.stream) {
     if (p.NT == 1) f = p.TG == 4 ? (const void*)k_router_fwd_stream<1, 4> : p.TG == 2 ? (const void*)k_router_fwd_stream<1, 2>
                                                                                     : (const void*)k_router_fwd_stream<1, 1>;
     else f = p.TG == 4 ? (const void*)k_router_fwd_stream<2, 4> : p.TG == 2 ? (const void*)k_router_fwd_stream<2, 2>
@@ -1554,6 +1754,24 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
       else MOE_FWDS(2, 1);
     }
 #undef MOE_FWDS
+    return check_launch("k_router_fwd_bf16");
+  }
+  if (mfma && p.wide) {
+    // wide streaming form: packed gate, finalize folded into the last block (ticket zero on entry and on exit)
+    i16x8* wp = reinterpret_cast<i16x8*>(ws + p.off_wp);
+    const int64_t lanes = (int64_t)(H / 32) * p.NT * 64;
+    MOE_LAUNCH("k_pack_gate", k_pack_gate, dim3((unsigned)std::min<int64_t>(1024, (lanes + 255) / 256)), dim3(256), 0, s,
+               static_cast<const uint16_t*>(wg), (int)H, (int)E, p.NT, wp, nullptr);
+    unsigned* ticket = reinterpret_cast<unsigned*>(ws + p.off_ticket);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+#define MOE_FWDW(NTv)                                                                                               \
+  MOE_LAUNCH("k_router_fwd_bf16", (k_router_fwd_wide<NTv>), dim3(p.nblk), dim3(512), 0, s, xb, wp, bias, (int)N,     \
+             (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz, ticket, aux_coef,   \
+             z_coef, cnt_out, stats_out, aux_out, z_out)
+    if (p.NT == 4) MOE_FWDW(4);
+    else if (p.NT == 8) MOE_FWDW(8);
+    else MOE_FWDW(16);
+#undef MOE_FWDW
     return check_launch("k_router_fwd_bf16");
   }
   if (mfma) {

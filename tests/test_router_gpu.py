@@ -29,8 +29,13 @@ SHAPES = [
     (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),   # ragged token count
     (64, 64, 8, 8, torch.bfloat16, torch.bfloat16),       # K == E
     (37, 128, 32, 1, torch.bfloat16, torch.bfloat16),     # K == 1, N < one block
-    (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # C3 expert count
-    (260, 512, 128, 8, torch.bfloat16, torch.bfloat16),   # C5 expert count
+    (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # C3 expert count (wide streaming kernel)
+    (4096, 2048, 64, 6, torch.bfloat16, torch.bfloat16),  # C3 shape, 32 blocks folded by the last one
+    (260, 512, 128, 8, torch.bfloat16, torch.bfloat16),   # C5 expert count (wide streaming kernel)
+    (200, 128, 256, 8, torch.bfloat16, torch.bfloat16),   # E = 256: 16 expert tiles
+    (150, 192, 160, 4, torch.bfloat16, torch.bfloat16),   # 128 < E < 256: padded tiles
+    (129, 320, 48, 5, torch.bfloat16, torch.bfloat16),    # 32 < E < 64: padded tiles, ragged block
+    (96, 96, 64, 4, torch.bfloat16, torch.bfloat16),      # H % 64 != 0 -> packed-gate kernel
     (100, 96, 10, 3, torch.bfloat16, torch.bfloat16),     # E not a multiple of 16
     (128, 256, 40, 18, torch.bfloat16, torch.bfloat16),   # K > 16 on the MFMA path
     (50, 72, 8, 2, torch.bfloat16, torch.bfloat16),       # H % 32 != 0 -> generic path
@@ -182,14 +187,15 @@ def test_router_empty_batch():
 
 
 def test_router_forward_workspace_reuse_across_paths():
-    """The streaming forward folds its finalize into the last block through a completion counter kept in the
-    reused (per stream) workspace.  Alternate shapes that take the streaming path, the packed-gate path and
+    """The streaming forwards fold their finalize into the last block through a completion counter kept in the
+    reused (per stream) workspace.  Alternate shapes that take the two streaming paths, the packed-gate path and
     the generic path on one stream, twice, and check every call's counts and statistics: a counter that a call
     leaves non-zero, or that another path overwrites, shows up as missing or stale statistics."""
     say("[router workspace reuse]")
     seq = [
         (16384, 4096, 8, 2, torch.bfloat16, torch.bfloat16),  # streaming, 256 blocks
-        (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # packed-gate kernel + finalize launch
+        (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # wide streaming, 3 blocks
+        (96, 96, 64, 4, torch.bfloat16, torch.bfloat16),      # packed-gate kernel + finalize launch
         (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),   # streaming, other block count
         (4096, 512, 8, 2, torch.float32, torch.float32),      # generic path
         (37, 512, 32, 1, torch.bfloat16, torch.bfloat16),     # streaming, a single block
