@@ -353,13 +353,16 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
   const int lane = tid & 63;
   // Per-expert sums over the blocks.  Thread (jj, q) = (tid / nq, tid % nq) owns V consecutive experts
   // (V = 4 when E % 4 == 0: one 16-byte load per array and block) and sums blocks jj, jj + nj, ... (experts
-  // fastest across lanes, so a load instruction reads consecutive experts of one block); thread e then folds
-  // the nj partial sums in jj order.
+  // fastest across lanes, so a load instruction reads consecutive experts of one block); a pairwise tree over
+  // jj in LDS then folds the nj partial sums (a fixed order for a given block count).
   {
     const bool quad = (E & 3) == 0;
     const int V = quad ? 4 : 1;
     const int nq = E / V;
-    const int nj = NTHR / nq;  // E <= kMaxE <= NTHR
+    // nj block strides: a power of two, at most NTHR / nq, and about nblk / 4 so each thread sums
+    // several blocks (loads in flight) and the tree fold below stays short
+    int nj = 1;
+    while (2 * nj * nq <= NTHR && 2 * nj <= (nblk + 3) / 4) nj *= 2;
     const int q = tid % nq;
     const int jj = tid / nq;
     int c[4] = {0, 0, 0, 0};
@@ -425,13 +428,17 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
       }
     }
     __syncthreads();
-    if (tid < E) {
-      int cs = s_pc[tid];
-      float ps = s_pp[tid];
-      for (int j = 1; j < nj; ++j) {
-        cs += s_pc[j * E + tid];
-        ps += s_pp[j * E + tid];
+    // pairwise tree over jj (fixed order): row j += row j + half
+    for (int half = nj >> 1; half > 0; half >>= 1) {
+      for (int i = tid; i < half * E; i += NTHR) {
+        s_pc[i] += s_pc[i + half * E];
+        s_pp[i] += s_pp[i + half * E];
       }
+      __syncthreads();
+    }
+    if (tid < E) {
+      const int cs = s_pc[tid];
+      const float ps = s_pp[tid];
       cnt_out[tid] = cs;
       s_c[tid] = (float)cs;
       s_pe[tid] = ps / (float)N;
@@ -1018,10 +1025,15 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
   for (int j = 0; j < EPL; ++j) p[j] *= inv;
   if (gw != nullptr) {
     // S = max(sum v, 1e-30); gwv = sum gw*v; grad_v = gw/S - gwv/S^2
+    // v_k = p[e_k], picked from this lane's registers (the lane holding e_k contributes, the row sums)
     float S = 0.f, gwv = 0.f;
     for (int k = 0; k < K; ++k) {
       const int e = (int)idx[(int64_t)t * K + k];
-      const float v = expf(logits[(int64_t)t * E + e] - m) * inv;
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) v = (e == sub + LPT * j) ? p[j] : v;
+#pragma unroll
+      for (int o = LPT / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
       const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
       S += v;
       gwv += gk * v;
