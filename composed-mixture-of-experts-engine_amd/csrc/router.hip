@@ -993,6 +993,28 @@ __device__ __forceinline__ GCoef glogit_coef(const float* __restrict__ grad_aux,
   return GCoef{aux_coef * ga * (float)E / (float)N, z_coef * gz * 2.f / (float)N, 1.f / ((float)N * (float)K)};
 }
 
+// Sum / max over the LPT lanes that share a token (DPP within a row of 16 lanes).
+template <int LPT>
+__device__ __forceinline__ float grp_sum(float v) {
+  if constexpr (LPT == 16) {
+    return row16_sum(v);
+  } else {
+#pragma unroll
+    for (int o = LPT / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+  }
+}
+template <int LPT>
+__device__ __forceinline__ float grp_max(float v) {
+  if constexpr (LPT == 16) {
+    return row16_max(v);
+  } else {
+#pragma unroll
+    for (int o = LPT / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+  }
+}
+
 template <int LPT, int EPL>
 __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, const int64_t* __restrict__ idx,
                                              const void* __restrict__ gw, int gw_dt,
@@ -1009,16 +1031,14 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
   float m = lg[0];
 #pragma unroll
   for (int j = 1; j < EPL; ++j) m = fmaxf(m, lg[j]);
-#pragma unroll
-  for (int o = LPT / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = grp_max<LPT>(m);
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     p[j] = expf(lg[j] - m);
     s += p[j];
   }
-#pragma unroll
-  for (int o = LPT / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  s = grp_sum<LPT>(s);
   const float inv = 1.f / s;
   const float lse = m + logf(s);
 #pragma unroll
@@ -1032,8 +1052,7 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
       float v = 0.f;
 #pragma unroll
       for (int j = 0; j < EPL; ++j) v = (e == sub + LPT * j) ? p[j] : v;
-#pragma unroll
-      for (int o = LPT / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      v = grp_sum<LPT>(v);
       const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
       S += v;
       gwv += gk * v;
@@ -1055,11 +1074,8 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
     inner += gp[j] * p[j];
     pf += p[j] * f[j];
   }
-#pragma unroll
-  for (int o = LPT / 2; o > 0; o >>= 1) {
-    inner += __shfl_xor(inner, o);
-    pf += __shfl_xor(pf, o);
-  }
+  inner = grp_sum<LPT>(inner);
+  pf = grp_sum<LPT>(pf);
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     float v = p[j] * (gp[j] - inner);
@@ -1102,7 +1118,7 @@ __global__ __launch_bounds__(256) void k_router_glogits(const float* __restrict_
         if (e < E) {
           float v = gl[j];
           if (round_bf16) v = bf2f(f2bf(v));
-          G[(int64_t)t * E + e] = v;
+          if (G) G[(int64_t)t * E + e] = v;
           if (gb) gb[(int64_t)t * ekp + e] = f2bf(v);
         }
       }
@@ -1444,6 +1460,183 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
       }
 }
 
+// ---------------------------------------------------------------------------
+// Backward 2, wide form (bf16 x bf16, 32 < E <= 128 as EK = 2 or 4 chunks of 32 experts, H % 256 == 0):
+// dx = G wg^T and the dwg partial x^T G of one (token chunk, 256 hidden columns) block, with G = dL/dlogits
+// in bf16 ([N, EKP], from k_router_glogits).  With many experts the fp32 dwg partials ([chunks, H, E]) are
+// as large as x unless the chunks are long, so each block covers ~N * nht / 256 tokens (about one block
+// per CU).  Per 32-token step the block stages the step's G rows in LDS (two buffers, one barrier per
+// step) and each wave works on its 64 hidden columns: the x tile goes to a wave-private LDS tile, the dwg
+// operands x^T (A) and G^T (B) are transposing reads of the x and G tiles, and dx (k = expert) takes G rows
+// as A and the gate rows (held in registers for the whole chunk) as B; dx is written back through the x
+// tile as 16-byte row segments.  x is prefetched two steps ahead, G one.
+// ---------------------------------------------------------------------------
+constexpr int kWideBwdBlocks = 256;  // target block count of the wide backward
+
+template <int EK>
+constexpr int wide_gpitch() { return EK == 4 ? 128 + 72 : EK * 32 + 8; }  // 36 dwords mod 64 between rows
+
+template <int EK, int NTE>
+__global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ wg,
+                                                          const uint16_t* __restrict__ gb, int N, int H, int E,
+                                                          int tc_len, int nht, uint16_t* __restrict__ dx,
+                                                          float* __restrict__ ws_dw) {
+  constexpr int EKP = EK * 32;
+  constexpr int GP = wide_gpitch<EK>();  // G tile pitch (bf16): 16-byte rows, conflict-free reads below
+  constexpr int GU = EKP / 8;            // 16-byte units per G row
+  constexpr int GPT = (32 * GU + 255) / 256;  // G units per thread per step
+  __shared__ __attribute__((aligned(16))) uint16_t gs[2][32 * GP];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[4][32 * kSXP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int g = lane >> 4;
+  const int n = lane & 15;
+  const int chunk = blockIdx.x / nht;
+  const int ht = blockIdx.x - chunk * nht;
+  const int tbeg = chunk * tc_len;
+  const int tend = min(N, tbeg + tc_len);
+  const int nst = ((tend - tbeg + 63) / 64) * 2;  // 32-token steps, rounded up to even
+  const int col0 = ht * 256 + wv * 64;            // this wave's first hidden column
+  uint16_t* xsw = xs[wv];
+
+  // x stream: lane loads rows (lane/8) + 8j of the step, 16-byte chunk lane%8 of the wave's 64 columns
+  // (rows past the chunk re-read its last row and are zeroed when written to LDS)
+  const uint16_t* xw = x + col0 + (lane & 7) * 8;
+  auto load_x = [&](u32x4(&r)[4], int ts0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = ts0 + (lane >> 3) + 8 * j;
+      r[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xw + (int64_t)min(t, tend - 1) * H));
+    }
+  };
+  // G stream: unit q = tid + 256 j of the step is row q / GU, 16-byte unit q % GU
+  auto load_g = [&](u32x4(&r)[GPT], int ts0) {
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      const int q = tid + 256 * j;
+      const int t = ts0 + q / GU;
+      r[j] = q < 32 * GU ? *reinterpret_cast<const u32x4*>(gb + (int64_t)min(t, tend - 1) * EKP + (q % GU) * 8)
+                         : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_g = [&](const u32x4(&r)[GPT], int ts0, uint16_t* gt) {
+#pragma unroll
+    for (int j = 0; j < GPT; ++j) {
+      const int q = tid + 256 * j;
+      if (q < 32 * GU) {
+        const bool ok = ts0 + q / GU < tend;
+        *reinterpret_cast<u32x4*>(&gt[(q / GU) * GP + (q % GU) * 8]) =
+            u32x4{ok ? r[j][0] : 0u, ok ? r[j][1] : 0u, ok ? r[j][2] : 0u, ok ? r[j][3] : 0u};
+      }
+    }
+  };
+  u32x4 xa[4], xb[4], ga[GPT];
+  load_x(xa, tbeg);
+  load_x(xb, tbeg + 32);
+  load_g(ga, tbeg);
+
+  // gate fragments for dx: B[k = e][n = h] = wg[h][e], e = 32 ek + 8 g + j (zero past E)
+  i16x8 wB[4][EK];
+#pragma unroll
+  for (int nc = 0; nc < 4; ++nc) {
+    const uint16_t* wr = wg + (int64_t)(col0 + nc * 16 + n) * E;
+#pragma unroll
+    for (int ek = 0; ek < EK; ++ek) {
+      const int e0 = ek * 32 + g * 8;
+      if ((E & 7) == 0 && e0 + 8 <= E) {  // 16-byte aligned row segment
+        wB[nc][ek] = *reinterpret_cast<const i16x8*>(wr + e0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wB[nc][ek][j] = e0 + j < E ? (short)wr[e0 + j] : (short)0;
+      }
+    }
+  }
+  f32x4 accw[4][NTE];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ne = 0; ne < NTE; ++ne) accw[mt][ne] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](u32x4(&r)[4], int s) {
+    const int lr0 = 32 * s;
+    uint16_t* gt = gs[s & 1];
+    store_g(ga, tbeg + lr0, gt);
+    if (s + 1 < nst) load_g(ga, tbeg + lr0 + 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = tbeg + lr0 + (lane >> 3) + 8 * j < tend;
+      const u32x4 v = r[j];
+      *reinterpret_cast<u32x4*>(&xsw[((lane >> 3) + 8 * j) * kSXP + (lane & 7) * 8]) =
+          u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
+    }
+    load_x(r, tbeg + lr0 + 64);
+    lds_sync();  // the step's G tile is visible to every wave (and every wave is done with step s-1)
+    // dwg: D[m = h][n = e] += sum_t x[t][h] G[t][e]; A = x^T and B = G^T from transposing reads
+    i16x8 bG[NTE];
+#pragma unroll
+    for (int ne = 0; ne < NTE; ++ne) {
+      const int cc = ne * 16 + 4 * (n & 3);
+      const sh4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sh4*)&gt[(8 * g + (n >> 2)) * GP + cc]);
+      const sh4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sh4*)&gt[(8 * g + 4 + (n >> 2)) * GP + cc]);
+      bG[ne] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int cc = mt * 16 + 4 * (n & 3);
+      const sh4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sh4*)&xsw[(8 * g + (n >> 2)) * kSXP + cc]);
+      const sh4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_sh4*)&xsw[(8 * g + 4 + (n >> 2)) * kSXP + cc]);
+      const i16x8 a = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int ne = 0; ne < NTE; ++ne)
+        accw[mt][ne] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, bG[ne]), accw[mt][ne]);
+    }
+    // dx: D[m = t][n = h] = sum_e G[t][e] wg[h][e], written over the x tile
+#pragma unroll
+    for (int mk = 0; mk < 2; ++mk) {
+      i16x8 aG[EK];
+#pragma unroll
+      for (int ek = 0; ek < EK; ++ek) aG[ek] = *reinterpret_cast<const i16x8*>(&gt[(mk * 16 + n) * GP + ek * 32 + g * 8]);
+#pragma unroll
+      for (int nc = 0; nc < 4; ++nc) {
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ek = 0; ek < EK; ++ek)
+          d = mfma16x16x32(__builtin_bit_cast(bf16x8, aG[ek]), __builtin_bit_cast(bf16x8, wB[nc][ek]), d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xsw[(mk * 16 + g * 4 + i) * kSXP + nc * 16 + n] = f2bf(d[i]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int lr = (lane >> 3) + 8 * j;
+      const int t = tbeg + lr0 + lr;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&xsw[lr * kSXP + (lane & 7) * 8]);
+      if (t < tend)
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dx + (int64_t)t * H + col0 + (lane & 7) * 8));
+    }
+  };
+
+  for (int s = 0; s < nst; s += 2) {
+    step(xa, s);
+    step(xb, s + 1);
+  }
+
+  float* out = ws_dw + (int64_t)chunk * H * E;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int ne = 0; ne < NTE; ++ne)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = col0 + mt * 16 + g * 4 + i;
+        const int e = ne * 16 + n;
+        if (e < E) out[(int64_t)h * E + e] = accw[mt][ne][i];
+      }
+}
+
 // Generic dx = G wg^T: one thread per (t, h).
 __global__ __launch_bounds__(256) void k_router_dx_generic(const float* __restrict__ G, const void* __restrict__ wg,
                                                            int w_dt, int N, int H, int E, void* __restrict__ dx,
@@ -1591,6 +1784,7 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt, bool allow
 struct BwdPlan {
   bool mfma;
   bool stream;  // k_router_dxdw_stream (E <= 32, H % 256 == 0)
+  bool wide;    // k_router_glogits + k_router_dxdw_wide (32 < E <= 128, H % 256 == 0)
   int EK, NTE;
   int nchunk, tc_len;
   size_t off_g, off_gb, off_ws, total;
@@ -1605,7 +1799,14 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   if (p.NTE == 3) p.NTE = 4;
   if (p.NTE > 4 && p.NTE < 8) p.NTE = 8;
   p.stream = p.mfma && E <= 32 && H % 256 == 0;
-  if (p.stream) {
+  p.wide = p.mfma && E > 32 && H % 256 == 0;
+  if (p.wide) {
+    // about one block per CU; long chunks keep the fp32 dwg partials few
+    const int nht = (int)(H / 256);
+    const int want = std::max(1, kWideBwdBlocks / nht);
+    p.tc_len = std::max(64, cdiv(cdiv(N, want), 64) * 64);
+    p.nchunk = cdiv(N, p.tc_len);
+  } else if (p.stream) {
     // ~768 blocks (three per CU); chunks of a multiple of 64 tokens, at most kSTC
     const int nht = (int)(H / 256);
     const int want = std::max(1, 768 / nht);
@@ -1872,6 +2073,33 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
     if (p.NTE == 1) MOE_DXDWS(1);
     else MOE_DXDWS(2);
 #undef MOE_DXDWS
+    if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+    launch_reduce(s, wsdw, nchunk, H * E, dwg_out, wg_dtype);
+    return check_launch("moe_router_bwd");
+  }
+  if (mfma && p.wide && aligned16(wg)) {
+    // wide form: dL/dlogits in bf16 only (16 lanes per token), then the streaming dx / dwg kernel
+    const int ekp = p.EK * 32;
+#define MOE_GLOGW(EPL)                                                                                         \
+  MOE_LAUNCH("k_router_glogits", (k_router_glogits<16, EPL>),                                                  \
+             dim3((unsigned)std::min<int64_t>(4096, (N * 16 + 255) / 256)), dim3(256), 0, s, logits, idx,      \
+             grad_w, gw_dtype, cnt, grad_aux, grad_z, aux_coef, z_coef, (int)N, (int)E, (int)K, 1,            \
+             static_cast<float*>(nullptr), gb, ekp)
+    if (E <= 64) MOE_GLOGW(4);
+    else MOE_GLOGW(8);
+#undef MOE_GLOGW
+    if (int rc = check_launch("k_router_glogits")) return rc;
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    const uint16_t* wb = static_cast<const uint16_t*>(wg);
+    uint16_t* dxb = static_cast<uint16_t*>(dx_out);
+    const int nht = (int)(H / 256);
+    const dim3 grid((unsigned)(p.nchunk * nht));
+    if (p.EK == 2)
+      MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_wide<2, 4>), grid, dim3(256), 0, s, xb, wb, gb, (int)N, (int)H,
+                 (int)E, p.tc_len, nht, dxb, wsdw);
+    else
+      MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_wide<4, 8>), grid, dim3(256), 0, s, xb, wb, gb, (int)N, (int)H,
+                 (int)E, p.tc_len, nht, dxb, wsdw);
     if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
     launch_reduce(s, wsdw, nchunk, H * E, dwg_out, wg_dtype);
     return check_launch("moe_router_bwd");

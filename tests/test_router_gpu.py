@@ -31,7 +31,9 @@ SHAPES = [
     (37, 128, 32, 1, torch.bfloat16, torch.bfloat16),     # K == 1, N < one block
     (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # C3 expert count (wide streaming kernel)
     (4096, 2048, 64, 6, torch.bfloat16, torch.bfloat16),  # C3 shape, 32 blocks folded by the last one
-    (260, 512, 128, 8, torch.bfloat16, torch.bfloat16),   # C5 expert count (wide streaming kernel)
+    (260, 512, 128, 8, torch.bfloat16, torch.bfloat16),   # C5 expert count (wide streaming kernels)
+    (8192, 2048, 128, 8, torch.bfloat16, torch.bfloat16), # C5 width: 32 backward chunks of 256 tokens
+    (200, 256, 50, 4, torch.bfloat16, torch.bfloat16),    # E % 8 != 0 on the wide kernels
     (200, 128, 256, 8, torch.bfloat16, torch.bfloat16),   # E = 256: 16 expert tiles
     (150, 192, 160, 4, torch.bfloat16, torch.bfloat16),   # 128 < E < 256: padded tiles
     (129, 320, 48, 5, torch.bfloat16, torch.bfloat16),    # 32 < E < 64: padded tiles, ragged block
