@@ -63,6 +63,7 @@ struct GemmArgs {
   int F;               // EPI1 / EPI2: ffn width
   const int* offsets;  // [E+1] row segments
   const int* tile_off; // [E+1] m-tile prefix (row-grouped, computed with this kernel's BM)
+  const int* korder;   // [E] expert order of the k-grouped tiles (heaviest first per XCD range)
   int E;
   int M, N, K;         // k-grouped: M, N fixed; row-grouped: N, K fixed
 };
@@ -208,8 +209,13 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     const int chunk = (total + 7) >> 3;
     L = xcd * chunk + slot;
     if (slot >= chunk || L >= total) return;
-    e = L / (Tm * Tn);
-    const int r = L - e * Tm * Tn;
+    // every expert has Tm * Tn tiles but a reduction as long as its row count: experts are taken in the
+    // order korder (dealt to the XCD ranges by decreasing rows, heaviest first within a range), so each
+    // XCD gets a similar share of the reduction work and its CUs, which take blocks in order, start on
+    // the longest tiles
+    const int p = L / (Tm * Tn);
+    e = g.korder[p];
+    const int r = L - p * Tm * Tn;
     // groups of (up to) 4 m-tiles, n walked within a group: the 32 tiles an XCD runs at once form a
     // 4 x 8 block that shares 12 operand panels per k slice (an n-fastest row of 32 tiles would need 33)
     constexpr int GM = 4;
@@ -484,14 +490,39 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   }
 }
 
-// tile_off[0] = 0, tile_off[e+1] = sum_{e' <= e} ceil(rows_e' / bm)  (one block, E <= 1024).
+// tile_off[0] = 0, tile_off[e+1] = sum_{e' <= e} ceil(rows_e' / bm)  (one block, E <= 1024), and the
+// expert order of the k-grouped products: experts ranked by rows (descending, lower id first on a tie) are
+// dealt to the 8 XCD ranges in snake order (rank r -> range r % 8 on even rounds, 7 - r % 8 on odd ones),
+// and korder lists range 0's experts by rank, then range 1's, ...
 __global__ __launch_bounds__(1024) void k_gemm_tiles(const int* __restrict__ offsets, int E, int bm,
-                                                     int* __restrict__ tile_off) {
+                                                     int* __restrict__ tile_off, int* __restrict__ korder) {
   __shared__ int part[1024];
+  __shared__ int rows[1024];
+  __shared__ int xcnt[8], xbase[8];
   const int tid = threadIdx.x;
-  const int c = tid < E ? (offsets[tid + 1] - offsets[tid] + bm - 1) / bm : 0;
+  const int nrow = tid < E ? offsets[tid + 1] - offsets[tid] : 0;
+  const int c = tid < E ? (nrow + bm - 1) / bm : 0;
   part[tid] = c;
+  rows[tid] = nrow;
+  if (tid < 8) xcnt[tid] = 0;
   __syncthreads();
+  int rank = 0, x = 0, j = 0;
+  if (tid < E) {
+    for (int f = 0; f < E; ++f) rank += (rows[f] > nrow || (rows[f] == nrow && f < tid)) ? 1 : 0;
+    j = rank >> 3;
+    x = (j & 1) ? 7 - (rank & 7) : (rank & 7);
+    atomicAdd(&xcnt[x], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int b = 0;
+    for (int q = 0; q < 8; ++q) {
+      xbase[q] = b;
+      b += xcnt[q];
+    }
+  }
+  __syncthreads();
+  if (tid < E) korder[xbase[x] + j] = tid;
   for (int o = 1; o < 1024; o <<= 1) {
     const int v = tid >= o ? part[tid - o] : 0;
     __syncthreads();
@@ -532,7 +563,7 @@ constexpr int kNW_fwd1 = MOE_GEMM_NW, kNW_fwd2 = MOE_GEMM_NW, kNW_dact = MOE_GEM
 
 using namespace moe;
 
-extern "C" size_t moe_swiglu_workspace(int64_t E) { return (size_t)((E + 1) * 4 + 255) & ~(size_t)255; }
+extern "C" size_t moe_swiglu_workspace(int64_t E) { return (size_t)((2 * E + 1) * 4 + 255) & ~(size_t)255; }
 
 extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_up, const void* w_down,
                               const int32_t* offsets, int64_t R, int64_t H, int64_t F, int64_t E, void* act,
@@ -547,7 +578,8 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   if (ws_bytes < moe_swiglu_workspace(E) || !workspace) return set_error("moe_swiglu_fwd: workspace"), MOE_EWORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int* tile_off = static_cast<int*>(workspace);
-  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off);
+  int* korder = tile_off + (E + 1);
+  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off, korder);
   GemmArgs a{};
   a.offsets = offsets;
   a.tile_off = tile_off;
@@ -597,7 +629,8 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
   if (ws_bytes < moe_swiglu_workspace(E) || !workspace) return set_error("moe_swiglu_bwd: workspace"), MOE_EWORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int* tile_off = static_cast<int*>(workspace);
-  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off);
+  int* korder = tile_off + (E + 1);
+  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off, korder);
   // dA: dh = epilogue(dy . Wd)   (B[n=f][k=h] = Wd[h][f])
   if (R > 0) {
     GemmArgs a{};
@@ -641,6 +674,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
   {
     GemmArgs a{};
     a.offsets = offsets;
+    a.korder = korder;
     a.E = (int)E;
     a.A = static_cast<const uint16_t*>(dy);
     a.lda = H;
@@ -657,6 +691,7 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
   {
     GemmArgs a{};
     a.offsets = offsets;
+    a.korder = korder;
     a.E = (int)E;
     a.A = static_cast<const uint16_t*>(dh);
     a.lda = 2 * F;
