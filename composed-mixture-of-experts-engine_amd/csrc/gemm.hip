@@ -86,7 +86,9 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // 16 zero bytes: the source of every DMA lane whose element lies past the reduction length.
 __device__ __attribute__((aligned(16))) const uint16_t g_zero16[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 
-__device__ __forceinline__ float silu_f(float g) { return g / (1.f + __expf(-g)); }
+// sigmoid(g) = 1 / (1 + e^-g) with the hardware reciprocal (~1 ulp of fp32; the results are rounded to bf16).
+__device__ __forceinline__ float sigmoid_f(float g) { return __builtin_amdgcn_rcpf(1.f + __expf(-g)); }
+__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_f(g); }
 
 // s_waitcnt vmcnt(n) (expcnt / lgkmcnt left unconstrained), gfx9 encoding.
 template <int N>
@@ -468,7 +470,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
           float o1[2], o2[2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const float sg = 1.f / (1.f + __expf(-gg[h]));
+            const float sg = sigmoid_f(gg[h]);
             const float sl = gg[h] * sg;
             o1[h] = da[h] * uu[h] * sg * (1.f + gg[h] * (1.f - sg));
             o2[h] = da[h] * sl;
