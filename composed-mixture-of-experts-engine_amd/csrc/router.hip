@@ -359,10 +359,10 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
     const bool quad = (E & 3) == 0;
     const int V = quad ? 4 : 1;
     const int nq = E / V;
-    // nj block strides: a power of two, at most NTHR / nq, and about nblk / 4 so each thread sums
+    // nj block strides: a power of two, at most NTHR / nq, and about nblk / 8 so each thread sums
     // several blocks (loads in flight) and the tree fold below stays short
     int nj = 1;
-    while (2 * nj * nq <= NTHR && 2 * nj <= (nblk + 3) / 4) nj *= 2;
+    while (2 * nj * nq <= NTHR && 2 * nj <= (nblk + 7) / 8) nj *= 2;
     const int q = tid % nq;
     const int jj = tid / nq;
     int c[4] = {0, 0, 0, 0};
@@ -372,16 +372,16 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
         const buf_rsrc_t rc = buf_rsrc(part_cnt, nblk * E * 4), rp = buf_rsrc(part_p, nblk * E * 4);
         constexpr int pol = COH ? kPolicyCoherent : 0;
         int b = jj;
-        for (; b + 3 * nj < nblk; b += 4 * nj) {  // 8 independent 16-byte loads in flight
-          u32x4 cv[4], pv[4];
+        for (; b + 7 * nj < nblk; b += 8 * nj) {  // 16 independent 16-byte loads in flight
+          u32x4 cv[8], pv[8];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < 8; ++u) {
             const int off = ((b + u * nj) * E + 4 * q) * 4;
             cv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, pol));
             pv[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, pol));
           }
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+          for (int u = 0; u < 8; ++u)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               c[i] += (int)cv[u][i];
@@ -474,22 +474,29 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
     s_red[1][tid >> 6] = nf;
   }
   __syncthreads();
-  if (tid == 0) {
+  if (tid < 64) {  // wave 0: the per-expert statistics in double, lane-strided then a fixed butterfly
+    double tot = 0.0, mx = 0.0, aux = 0.0;
+    for (int e = tid; e < E; e += 64) {
+      const double c = s_c[e];
+      tot += c;
+      mx = fmax(mx, c);
+      aux += (c / ((double)N * K)) * (double)s_pe[e];
+    }
+    tot = wave_sum(tot);
+    aux = wave_sum(aux);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
+    const double mean = tot / E;
+    double var = 0.0;
+    for (int e = tid; e < E; e += 64) var += ((double)s_c[e] - mean) * ((double)s_c[e] - mean);
+    var = wave_sum(var);
+    if (tid != 0) return;
     z = s_red[0][0];
     nf = s_red[1][0];
     for (int w = 1; w < NTHR / 64; ++w) {
       z += s_red[0][w];
       nf += s_red[1][w];
     }
-    double tot = 0.0, mx = 0.0, aux = 0.0;
-    for (int e = 0; e < E; ++e) {
-      tot += s_c[e];
-      mx = fmax(mx, (double)s_c[e]);
-      aux += ((double)s_c[e] / ((double)N * K)) * (double)s_pe[e];
-    }
-    const double mean = tot / E;
-    double var = 0.0;
-    for (int e = 0; e < E; ++e) var += ((double)s_c[e] - mean) * ((double)s_c[e] - mean);
     const float zstat = z / (float)N;
     const float aux_raw = (float)(aux * E);
     stats[0] = zstat;
@@ -744,7 +751,8 @@ struct WideFwd {
   static constexpr int XI = XB / 8192;   // x DMA instructions per wave per slice
   static constexpr int GI = GB / 8192;   // gate DMA instructions per wave per slice
   static constexpr int GPS = XI + GI;
-  static constexpr int kSlots = NT == 4 ? 6 : (NT == 8 ? 4 : 3);  // <= 144 KB of ring
+  // NT == 4: 3 slots (72 KB) let two blocks share a CU, so one block's routing overlaps the other's stream
+  static constexpr int kSlots = NT == 4 ? 3 : (NT == 8 ? 4 : 3);
 };
 
 template <int GPS>
