@@ -11,6 +11,9 @@ timing starts; ``moe_mi355/configs.py``):
           GEMM, combine, and the whole backward.  ``value`` = tokens/s.
   router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2 (always measured too,
           reported under "router").
+  norm_router  C2 shape with the block's RMSNorm in front of the router:
+          the norm fused into the router's read of the hidden state, fwd+bwd,
+          beside the unfused composition and a torch-ops norm.
   dispatch C3: router + planner + permute + combine forward, T=65536 d=2048
           E=64 K=6, cf=1.25 with drops.
   skewed  C5: layer fwd+bwd, T=32768 d=2048 E=128 F=768 K=8, cf=1.0 drops,
@@ -324,6 +327,76 @@ def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=64, budget_s=15.0):
 
 
 # ---------------------------------------------------------------------------
+# RMSNorm fused into the router read (C2 shape)
+# ---------------------------------------------------------------------------
+def norm_router_bytes(N, H, E, K):
+    """Algorithmic HBM bytes of the fused norm+router forward launch and of one fused fwd+bwd step.
+
+    Forward: read x, write xn, the router's per-token outputs (logits, lse, rstd, idx, w).  Backward: the
+    router backward reads xn and writes its dxn (two [N,H] passes), the norm backward reads x, the expert
+    path's dxn and the router's dxn and writes dx (four passes)."""
+    tok = N * E * 4 + N * 4 + N * 4 + N * K * (8 + 2)
+    fwd = 2 * N * H * 2 + H * E * 2 + H * 4 + tok
+    bwd = 6 * N * H * 2 + 2 * H * E * 2 + H * E * 4 + N * E * 4 + N * K * (8 + 2) + E * 8 + 2 * H * 4
+    return {"k_rmsnorm_route": fwd, "step": fwd + bwd}
+
+
+def run_norm_router(args, torch):
+    from moe_mi355 import configs
+    from moe_mi355.norm import NormRouterCore, RMSNormFn
+    from moe_mi355.router import RouterCore
+
+    cfg = configs.C2
+    dev = torch.device("cuda:0")
+    inp = configs.router_inputs(cfg)
+    N, H, E, K = cfg.T, cfg.H, cfg.E, cfg.K
+    eps = 1e-5
+    g = torch.Generator().manual_seed(77)
+    x = inp["x"].to(dev).requires_grad_(True)
+    gate = inp["gate_w"].to(dev).requires_grad_(True)
+    nw = (1.0 + 0.1 * torch.randn(H, generator=g)).to(dev).requires_grad_(True)
+    g_w = inp["grad_w"].to(dev)
+    g_xn = (torch.randn(N, H, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+
+    def fused():
+        xn, _i, w, *_ = NormRouterCore.apply(x, nw, eps, gate, K, 0.0, 0.0, None)
+        torch.autograd.grad((xn, w), (x, nw, gate), grad_outputs=(g_xn, g_w))
+
+    def composed():
+        xn = RMSNormFn.apply(x, nw, eps)
+        out = RouterCore.apply(xn, gate, K, 0.0, 0.0, None)
+        torch.autograd.grad((xn, out[1]), (x, nw, gate), grad_outputs=(g_xn, g_w))
+
+    def torch_norm():
+        # the reference's RMSNorm as torch ops (moe-engine/pkg/models/moe.py L:83-86) in front of the router
+        v = x.float()
+        xn = ((v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + eps)) * nw).to(x.dtype)
+        out = RouterCore.apply(xn, gate, K, 0.0, 0.0, None)
+        torch.autograd.grad((xn, out[1]), (x, nw, gate), grad_outputs=(g_xn, g_w))
+
+    steps = max(args.steps, 20)
+    ms, prof = timed(torch, fused, steps, args.warmup)
+    gms = graph_timed(torch, fused, steps, args.warmup)
+    ms_comp, _ = timed(torch, composed, steps, args.warmup, prof_steps=1)
+    ms_torch, _ = timed(torch, torch_norm, steps, args.warmup, prof_steps=1)
+    alg = norm_router_bytes(N, H, E, K)
+    kernels = kernel_table(prof, alg, 1e9, "GBps")
+    dom = "k_rmsnorm_route"
+    achieved = kernels[dom]["GBps"]
+    return {
+        "workload": "C2 RMSNorm + router fwd+bwd (norm fused into the router read)", "tokens": N, "d_model": H,
+        "experts": E, "top_k": K, "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
+        "fwd_bwd_GBps": round(alg["step"] / (ms * 1e-3) / 1e9, 1), "graph_ms_per_step": gms,
+        "unfused_ms_per_step": ms_comp, "torch_norm_ms_per_step": ms_torch,
+        "alg_bytes_per_step": alg["step"],
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom, cfg.name),
+                     "alg_bytes_per_launch": alg[dom], "avg_us": kernels[dom]["avg_us"]},
+        "kernels": kernels,
+    }
+
+
+# ---------------------------------------------------------------------------
 # dispatch (C3)
 # ---------------------------------------------------------------------------
 def run_dispatch(args, torch):
@@ -362,7 +435,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="layer", choices=["layer", "router", "dispatch", "skewed", "all"])
+    ap.add_argument("--workload", default="layer", choices=["layer", "router", "norm_router", "dispatch", "skewed", "all"])
     ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -405,6 +478,12 @@ def main():
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "top_k")}
+    elif args.workload == "norm_router":
+        main_res = run_norm_router(args, torch)
+        cpu = None
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "top_k")}
     elif args.workload == "dispatch":
         main_res = run_dispatch(args, torch)
         cpu = None
@@ -419,6 +498,7 @@ def main():
         roof = main_res.pop("roofline")
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
     if args.workload == "all":
+        extra["norm_router"] = run_norm_router(args, torch)
         extra["dispatch"] = run_dispatch(args, torch)
         extra["skewed"] = run_layer(args, torch, configs.C5, "routed", configs.layer_inputs(configs.C5))
     main_res.pop("ms_per_step", None)

@@ -126,6 +126,108 @@ def router_backward(
 
 
 # ---------------------------------------------------------------------------
+# RMSNorm in front of the router
+# ---------------------------------------------------------------------------
+def rmsnorm_forward(x: torch.Tensor, weight: torch.Tensor, eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``xn = ((x * rsqrt(mean(x^2) + eps)) * weight).to(x.dtype)`` over the last dim of ``x [N, H]``.
+
+    Returns ``(xn [N,H] x.dtype, rstd f32 [N])``."""
+    dev = L.require_device(x, weight)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    N, H = x.shape
+    xn = torch.empty_like(x)
+    rstd = torch.empty((N,), dtype=torch.float32, device=dev)
+    if N == 0:
+        return xn, rstd
+    rc = L.load().moe_rmsnorm_fwd(x.data_ptr(), L.dtype_code(x.dtype), weight.data_ptr(),
+                                  L.dtype_code(weight.dtype), float(eps), N, H, xn.data_ptr(), rstd.data_ptr(),
+                                  L.stream_of(dev))
+    L.check(rc, "moe_rmsnorm_fwd")
+    return xn, rstd
+
+
+def rmsnorm_router_forward(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float,
+    gate_w: torch.Tensor,
+    k: int,
+    bias: Optional[torch.Tensor] = None,
+    aux_coef: float = 0.0,
+    z_coef: float = 0.0,
+) -> Tuple[torch.Tensor, ...]:
+    """The norm and the router forward over its output in one call (one read of ``x`` from HBM for bf16 x and
+    gate with E <= 16).  Returns ``(xn, rstd, idx, w, logits, lse, cnt, stats, aux, z)`` with the outputs of
+    :func:`rmsnorm_forward` and :func:`router_forward` (``with_losses=True``)."""
+    dev = L.require_device(x, weight, gate_w, bias)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    gate_w = gate_w.contiguous()
+    N, H = x.shape
+    H2, E = gate_w.shape
+    if H != H2:
+        raise ValueError(f"rmsnorm_router_forward: hidden dims differ ({H} vs {H2})")
+    if bias is not None:
+        bias = bias.detach().to(torch.float32).contiguous()
+    lib = L.load()
+    xdt, gdt, wdt = L.dtype_code(x.dtype), L.dtype_code(weight.dtype), L.dtype_code(gate_w.dtype)
+    xn = torch.empty_like(x)
+    rstd = torch.empty((N,), dtype=torch.float32, device=dev)
+    idx = torch.empty((N, k), dtype=torch.int64, device=dev)
+    w = torch.empty((N, k), dtype=x.dtype, device=dev)
+    logits = torch.empty((N, E), dtype=torch.float32, device=dev)
+    lse = torch.empty((N,), dtype=torch.float32, device=dev)
+    cnt = torch.empty((E,), dtype=torch.int64, device=dev)
+    stats = torch.empty((L.STATS_HEAD + E,), dtype=torch.float32, device=dev)
+    aux = torch.empty((), dtype=torch.float32, device=dev)
+    z = torch.empty((), dtype=torch.float32, device=dev)
+    if N == 0:
+        for t in (cnt, stats, aux, z):
+            t.zero_()
+        return xn, rstd, idx, w, logits, lse, cnt, stats, aux, z
+    nbytes = lib.moe_rmsnorm_router_fwd_workspace(N, H, E, k, xdt, wdt)
+    ws = L.workspace(nbytes, dev, key="router_fwd")  # zeroed once; the kernels leave the counter at zero
+    rc = lib.moe_rmsnorm_router_fwd(
+        x.data_ptr(), xdt, weight.data_ptr(), gdt, float(eps), gate_w.data_ptr(), wdt, L.ptr(bias), N, H, E, k,
+        xn.data_ptr(), rstd.data_ptr(), idx.data_ptr(), w.data_ptr(), xdt, logits.data_ptr(), lse.data_ptr(),
+        cnt.data_ptr(), stats.data_ptr(), float(aux_coef), float(z_coef), aux.data_ptr(), z.data_ptr(),
+        ws.data_ptr(), nbytes, L.stream_of(dev),
+    )
+    L.check(rc, "moe_rmsnorm_router_fwd")
+    return xn, rstd, idx, w, logits, lse, cnt, stats, aux, z
+
+
+def rmsnorm_backward(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    rstd: torch.Tensor,
+    dxn: torch.Tensor,
+    dxn2: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Backward of :func:`rmsnorm_forward` for the gradient ``dxn (+ dxn2)`` of its output: ``(dx, dweight)``."""
+    dev = L.require_device(x, weight, rstd, dxn, dxn2)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    dxn = dxn.contiguous().to(x.dtype)
+    if dxn2 is not None:
+        dxn2 = dxn2.contiguous().to(x.dtype)
+    N, H = x.shape
+    dx = torch.empty_like(x)
+    dweight = torch.empty_like(weight)
+    lib = L.load()
+    nbytes = lib.moe_rmsnorm_bwd_workspace(N, H)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_rmsnorm_bwd(
+        x.data_ptr(), L.dtype_code(x.dtype), weight.data_ptr(), L.dtype_code(weight.dtype), rstd.data_ptr(),
+        dxn.data_ptr(), L.ptr(dxn2), N, H, dx.data_ptr(), dweight.data_ptr(), ws.data_ptr(), nbytes,
+        L.stream_of(dev),
+    )
+    L.check(rc, "moe_rmsnorm_bwd")
+    return dx, dweight
+
+
+# ---------------------------------------------------------------------------
 # Dispatch planner, permute, combine
 # ---------------------------------------------------------------------------
 LAYOUT_REFERENCE = 0

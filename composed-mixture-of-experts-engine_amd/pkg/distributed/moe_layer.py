@@ -216,8 +216,22 @@ class DistributedMoELayer(nn.Module):
             raise ValueError(f"tokens must be rank 2 or 3, got {tokens.dim()}")
         H = tokens.shape[-1]
         flat = tokens.reshape(-1, H)
-        N = flat.shape[0]
         idx, weights, _cnt = self.router(flat)
+        return self._experts_forward(flat, idx, weights).reshape(original_shape)
+
+    def forward_normed(self, tokens: torch.Tensor, norm_weight: torch.Tensor, eps: float) -> torch.Tensor:
+        """``forward(rmsnorm(tokens))`` with the norm fused into the router's read of the hidden state
+        (moe-engine/pkg/models/moe.py L:125-126): the normalised rows feed both the router and the experts."""
+        original_shape = tokens.shape
+        if tokens.dim() not in (2, 3):
+            raise ValueError(f"tokens must be rank 2 or 3, got {tokens.dim()}")
+        H = tokens.shape[-1]
+        flat = tokens.reshape(-1, H)
+        xn, idx, weights, _cnt = self.router.forward_with_norm(flat, norm_weight, eps)
+        return self._experts_forward(xn, idx, weights).reshape(original_shape)
+
+    def _experts_forward(self, flat: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
+        N = flat.shape[0]
         capacity = (
             math.ceil(self.capacity_factor * N * self.top_k / self.num_experts) if self.capacity_dropping else -1
         )
@@ -232,7 +246,7 @@ class DistributedMoELayer(nn.Module):
                 "NaN detected in DistributedMoELayer output after combine step. "
                 "Check expert FFN numerics and router weights."
             )
-        return out.reshape(original_shape)
+        return out
 
     def _forward_per_expert(self, flat: torch.Tensor, weights: torch.Tensor, p: ops.Plan) -> torch.Tensor:
         """Dispatch/combine kernels around per-expert module calls (custom experts, non-bf16 dtypes)."""

@@ -41,6 +41,7 @@ import torch
 
 from moe_mi355 import _lib, ops
 from moe_mi355.router import STAT_CNT_MEAN, STAT_CNT_STD, STAT_CNT_TOTAL, STAT_IMBALANCE, STAT_NONFINITE, STAT_Z
+from moe_mi355.norm import NormRouterCore
 from moe_mi355.router import RouterCore
 
 # Kept for import compatibility: True when the native gfx950 library is built
@@ -204,12 +205,32 @@ class MoERouter(torch.nn.Module):
         if force_reference:
             _no_reference_path()
 
+        idx, w, aux, z, logits, cnt, stats = RouterCore.apply(
+            flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, self._logit_bias()
+        )
+        return self._finish(flat, idx, w, aux, z, logits, cnt, stats)
+
+    def forward_with_norm(self, tokens: torch.Tensor, norm_weight: torch.Tensor, eps: float):
+        """Route ``rmsnorm(tokens)`` with the norm fused into the router's read of ``tokens``
+        (moe-engine/pkg/models/moe.py L:83-86, L:125-126).  Returns ``(xn, topk_idx, topk_w, dispatch_cnt)``:
+        ``xn`` is the normalised input the routing used, for the expert path."""
+        flat = tokens.reshape(-1, tokens.shape[-1])
+        assert flat.shape[1] == self.hidden_dim
+        xn, idx, w, aux, z, logits, cnt, stats = NormRouterCore.apply(
+            flat, norm_weight, float(eps), self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef,
+            self._logit_bias(),
+        )
+        idx, w, cnt = self._finish(flat, idx, w, aux, z, logits, cnt, stats)
+        return xn, idx, w, cnt
+
+    def _logit_bias(self):
         bias = self.bias
         if self.logit_bias is not None:
             bias = self.logit_bias if bias is None else bias.detach().float() + self.logit_bias
-        idx, w, aux, z, logits, cnt, stats = RouterCore.apply(
-            flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, bias
-        )
+        return bias
+
+    def _finish(self, flat, idx, w, aux, z, logits, cnt, stats):
+        N = flat.shape[0]
         if self.bias is not None:
             # Reference semantics (L:677-687): with a bias the combine weights are
             # recomputed under no_grad, so no gradient flows through w.

@@ -199,6 +199,40 @@ int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* 
                    int64_t F, int64_t E, void* dh, void* dxp, void* dw_gate, void* dw_up, void* dw_down,
                    void* workspace, size_t ws_bytes, void* stream);
 
+/* ----------------------------------------------------------------------
+ * RMSNorm in front of the router (the caller step before the routed path):
+ * replaces RMSNorm.forward (moe-engine/pkg/models/moe.py L:83-86) as used by
+ * ToyMoEBlock.forward (L:125-126, x + moe(norm(x))):
+ *   xn = ((x * rsqrt(mean_h(x^2) + eps)) * gamma).to(x.dtype), fp32 arithmetic;
+ * rstd_out [N] f32 keeps rsqrt(mean_h(x^2) + eps) for the backward.
+ * x / xn dtype MOE_F32 or MOE_BF16, gamma MOE_F32 or MOE_BF16; 8 <= H <= 8192,
+ * H % 8 == 0; x, gamma, xn 16-byte aligned.
+ *
+ * moe_rmsnorm_router_fwd: the norm with the router forward of moe_router_fwd
+ * applied to xn (same outputs, statistics, workspace contract and first-word
+ * completion counter).  For bf16 x and gate with E <= 16 one kernel reads x
+ * from HBM once, producing xn and the routing; otherwise the norm kernel runs
+ * first and the router kernels read xn.
+ *
+ * moe_rmsnorm_bwd: dx = rstd (g - xhat mean_h(g xhat)), xhat = x rstd,
+ * g = gamma * (dxn + dxn2) (dxn2 optional: a second gradient of xn, e.g. the
+ * router's, summed in fp32 inside the kernel); dgamma = sum_t (dxn + dxn2) xhat
+ * in gamma's dtype, summed in a fixed order (deterministic).
+ * ---------------------------------------------------------------------- */
+int moe_rmsnorm_fwd(const void* x, int x_dtype, const void* gamma, int gamma_dtype, float eps, int64_t N,
+                    int64_t H, void* xn_out, float* rstd_out, void* stream);
+size_t moe_rmsnorm_router_fwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
+int moe_rmsnorm_router_fwd(const void* x, int x_dtype, const void* gamma, int gamma_dtype, float eps,
+                           const void* wg, int wg_dtype, const float* bias, int64_t N, int64_t H, int64_t E,
+                           int64_t K, void* xn_out, float* rstd_out, int64_t* idx_out, void* w_out, int w_dtype,
+                           float* logits_out, float* lse_out, int64_t* cnt_out, float* stats_out, float aux_coef,
+                           float z_coef, float* aux_out, float* z_out, void* workspace, size_t ws_bytes,
+                           void* stream);
+size_t moe_rmsnorm_bwd_workspace(int64_t N, int64_t H);
+int moe_rmsnorm_bwd(const void* x, int x_dtype, const void* gamma, int gamma_dtype, const float* rstd,
+                    const void* dxn, const void* dxn2, int64_t N, int64_t H, void* dx_out, void* dgamma_out,
+                    void* workspace, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
