@@ -1119,7 +1119,8 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
                                                             const float* __restrict__ grad_z, float aux_coef,
                                                             float z_coef, int N, int H, int E, int K, int tc_len,
                                                             int nht, uint16_t* __restrict__ dx,
-                                                            float* __restrict__ ws_dw) {
+                                                            float* __restrict__ ws_dw, uint16_t* __restrict__ g_out,
+                                                            int g_pitch) {
   constexpr int GP = 32 + 8;         // token-major G row pitch (32 expert slots)
   constexpr int GTP = kSTC + 8;      // expert-major G row pitch
   __shared__ __attribute__((aligned(16))) uint16_t gs[kSTC * GP];
@@ -1182,6 +1183,12 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
       }
 #pragma unroll
       for (int e = 0; e < NTE * 16; ++e) gts[e * GTP + r] = e < E ? f2bf(gl[e]) : (uint16_t)0;
+      // the first column block of each chunk also hands G (bf16, g_pitch <= 16 expert slots) to the caller
+      if (g_out != nullptr && ht == 0 && t < tend) {
+        for (int c8 = 0; c8 < g_pitch; c8 += 8)
+          *reinterpret_cast<u32x4*>(g_out + (int64_t)t * g_pitch + c8) =
+              *reinterpret_cast<const u32x4*>(&gs[r * GP + c8]);
+      }
     }
   }
 
@@ -1230,6 +1237,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
         accw[mt][ne] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), accw[mt][ne]);
       }
     }
+    if (dx == nullptr) return;  // dwg only (the caller forms dx from G itself)
     // dx: D[m = t][n = h] = sum_e G[t][e] wg[h][e], written over the x tile
 #pragma unroll
     for (int mk = 0; mk < 2; ++mk) {
@@ -1402,6 +1410,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __rest
       for (int ne = 0; ne < NTE; ++ne)
         accw[mt][ne] = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, bG[ne]), accw[mt][ne]);
     }
+    if (dx == nullptr) return;  // dwg only (the caller forms dx from G itself)
     // dx: D[m = t][n = h] = sum_e G[t][e] wg[h][e], written over the x tile
 #pragma unroll
     for (int mk = 0; mk < 2; ++mk) {
@@ -1679,10 +1688,11 @@ template <int NTE>
 void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, const float* logits, const int64_t* idx,
                         const void* gw, int gw_dt, const int64_t* cnt, const float* grad_aux, const float* grad_z,
                         float aux_coef, float z_coef, int N, int H, int E, int K, int tc_len, int nchunk, uint16_t* dx,
-                        float* ws) {
+                        float* ws, uint16_t* g_out = nullptr, int g_pitch = 0) {
   const int nht = H / 256;
-  MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)), dim3(256), 0, s, x, wg,
-             logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K, tc_len, nht, dx, ws);
+  MOE_LAUNCH(dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)),
+             dim3(256), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K, tc_len,
+             nht, dx, ws, g_out, g_pitch);
 }
 
 template <int EK, int NTE>
@@ -1692,6 +1702,27 @@ void launch_dxdw(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* wg
 }
 
 }  // namespace
+
+bool router_dw_g_applies(int64_t H, int64_t E) { return E <= 16 && H % 256 == 0; }
+
+size_t router_dw_g_workspace(int64_t N, int64_t H, int64_t E) {
+  const BwdPlan p = plan_bwd(N > 0 ? N : 1, H, E, MOE_BF16, MOE_BF16);
+  return align256((size_t)p.nchunk * H * E * sizeof(float));
+}
+
+int router_dw_g(const uint16_t* x, const uint16_t* wg, const float* logits, const int64_t* idx, const void* grad_w,
+                int gw_dtype, const int64_t* cnt, const float* grad_aux, const float* grad_z, float aux_coef,
+                float z_coef, int64_t N, int64_t H, int64_t E, int64_t K, void* dwg_out, uint16_t* g_out, int g_pitch,
+                void* ws, hipStream_t s) {
+  const BwdPlan p = plan_bwd(N, H, E, MOE_BF16, MOE_BF16);
+  float* wsdw = static_cast<float*>(ws);
+  launch_dxdw_stream<1>(s, x, wg, logits, idx, grad_w, gw_dtype, cnt, grad_aux, grad_z, aux_coef, z_coef, (int)N,
+                        (int)H, (int)E, (int)K, p.tc_len, p.nchunk, nullptr, wsdw, g_out, g_pitch);
+  if (int rc = check_launch("k_router_dw_bf16")) return rc;
+  launch_reduce(s, wsdw, p.nchunk, H * E, dwg_out, MOE_BF16);
+  return check_launch("router_dw_g");
+}
+
 }  // namespace moe
 
 using namespace moe;

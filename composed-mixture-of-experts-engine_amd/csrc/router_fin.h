@@ -205,4 +205,17 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
   }
 }
 
+// ---------------------------------------------------------------------------
+// Router backward without dx, for callers that form dx from G themselves (the norm-fused backward):
+// dwg = x^T G reduced over token chunks into dwg_out (bf16 [H, E]), and G = dL/dlogits rounded to bf16
+// written to g_out ([N, g_pitch], experts past E zero; g_pitch = 8 or 16).  Applies to bf16 x and gate
+// with E <= 16 and H % 256 == 0; ws holds router_dw_g_workspace(N, H, E) bytes.
+// ---------------------------------------------------------------------------
+bool router_dw_g_applies(int64_t H, int64_t E);
+size_t router_dw_g_workspace(int64_t N, int64_t H, int64_t E);
+int router_dw_g(const uint16_t* x, const uint16_t* wg, const float* logits, const int64_t* idx, const void* grad_w,
+                int gw_dtype, const int64_t* cnt, const float* grad_aux, const float* grad_z, float aux_coef,
+                float z_coef, int64_t N, int64_t H, int64_t E, int64_t K, void* dwg_out, uint16_t* g_out, int g_pitch,
+                void* ws, hipStream_t s);
+
 }  // namespace moe

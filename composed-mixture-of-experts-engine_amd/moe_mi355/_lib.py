@@ -59,6 +59,12 @@ _SIGNATURES = {
     ),
     "moe_rmsnorm_bwd_workspace": (_SZ, [_I64, _I64]),
     "moe_rmsnorm_bwd": (_I32, [_P, _I32, _P, _I32, _P, _P, _P, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "moe_rmsnorm_router_bwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
+    "moe_rmsnorm_router_bwd": (
+        _I32,
+        [_P, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _F32, _F32, _P, _I64, _I64, _I64, _I64,
+         _P, _P, _P, _P, _SZ, _P],
+    ),
     "moe_swiglu_workspace": (_SZ, [_I64]),
     "moe_swiglu_fwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "moe_swiglu_bwd": (

@@ -4,9 +4,10 @@
                     (moe-engine/pkg/models/moe.py L:83-86, the norm of ToyMoEBlock L:125-126).
 ``NormRouterCore``  the norm with the router forward fused onto its output: one read of the hidden state
                     for both (bf16 x and gate, E <= 16), returning ``xn`` for the expert path together with
-                    everything :class:`moe_mi355.router.RouterCore` returns.  Its backward runs the router
-                    backward on ``xn`` and hands the router's dxn to the norm backward, which adds it to the
-                    expert path's gradient of ``xn`` inside the kernel (no separate gradient sum).
+                    everything :class:`moe_mi355.router.RouterCore` returns.  Its backward is one call
+                    (ops.rmsnorm_router_backward): the router's weight gradient over ``xn`` and dL/dlogits,
+                    then the norm backward, which forms the router's gradient of ``xn`` from dL/dlogits and
+                    the gate inside the kernel and adds the expert path's (no [N, H] gradient in between).
 """
 
 from __future__ import annotations
@@ -55,17 +56,20 @@ class NormRouterCore(torch.autograd.Function):
     def backward(ctx, g_xn, g_idx, g_w, g_aux, g_z, g_logits, g_cnt, g_stats):
         x, norm_weight, rstd, xn, gate_w, logits, idx, cnt = ctx.saved_tensors
         need_x, need_nw, need_gw = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[3]
-        dxn_router, dgate = None, None
+        dx = dnw = dgate = None
         if g_w is not None or g_aux is not None or g_z is not None:
+            # the router backward and the norm backward in one call: the router's gradient of xn is formed
+            # inside the norm kernel
             aux_coef = ctx.aux_coef if g_aux is not None else 0.0
             z_coef = ctx.z_coef if g_z is not None else 0.0
-            dxn_router, dgate = ops.router_backward(xn, gate_w, logits, idx, g_w, cnt, g_aux, g_z, aux_coef, z_coef)
-        dx = dnw = None
-        if need_x or need_nw:
-            if g_xn is None and dxn_router is None:
+            dx, dnw, dgate = ops.rmsnorm_router_backward(x, norm_weight, rstd, xn, gate_w, logits, idx, g_w, g_xn,
+                                                         cnt, g_aux, g_z, aux_coef, z_coef)
+        elif need_x or need_nw:
+            if g_xn is None:
                 dx, dnw = torch.zeros_like(x), torch.zeros_like(norm_weight)
             else:
-                first, second = (g_xn, dxn_router) if g_xn is not None else (dxn_router, None)
-                dx, dnw = ops.rmsnorm_backward(x, norm_weight, rstd, first, second)
+                dx, dnw = ops.rmsnorm_backward(x, norm_weight, rstd, g_xn)
+        if need_gw and dgate is None:
+            dgate = torch.zeros_like(gate_w)
         return (dx if need_x else None), (dnw if need_nw else None), None, (dgate if need_gw else None), \
             None, None, None, None

@@ -227,6 +227,65 @@ def rmsnorm_backward(
     return dx, dweight
 
 
+def rmsnorm_router_backward(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    rstd: torch.Tensor,
+    xn: torch.Tensor,
+    gate_w: torch.Tensor,
+    logits: torch.Tensor,
+    idx: torch.Tensor,
+    grad_w: Optional[torch.Tensor],
+    dxn: Optional[torch.Tensor],
+    cnt: Optional[torch.Tensor] = None,
+    grad_aux: Optional[torch.Tensor] = None,
+    grad_z: Optional[torch.Tensor] = None,
+    aux_coef: float = 0.0,
+    z_coef: float = 0.0,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of :func:`rmsnorm_router_forward` for the router's upstream gradients (as
+    :func:`router_backward`) and a gradient ``dxn`` of ``xn`` from the expert path (or None).
+
+    Returns ``(dx [N,H] x.dtype, dweight [H] weight.dtype, dgate_w [H,E] gate_w.dtype)``."""
+    dev = L.require_device(x, weight, rstd, xn, gate_w, logits, idx, grad_w, dxn, cnt)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    xn = xn.contiguous()
+    gate_w = gate_w.contiguous()
+    logits = logits.contiguous()
+    idx = idx.contiguous()
+    if dxn is not None:
+        dxn = dxn.contiguous().to(x.dtype)
+    N, H = x.shape
+    E = gate_w.shape[1]
+    K = idx.shape[1]
+    lib = L.load()
+    xdt, ndt, wdt = L.dtype_code(x.dtype), L.dtype_code(weight.dtype), L.dtype_code(gate_w.dtype)
+    gdt = L.MOE_F32
+    if grad_w is not None:
+        grad_w = grad_w.contiguous()
+        if grad_w.dtype not in (torch.float32, torch.bfloat16):
+            grad_w = grad_w.float()
+        gdt = L.dtype_code(grad_w.dtype)
+    if grad_aux is not None:
+        grad_aux = grad_aux.detach().to(torch.float32).reshape(1).contiguous()
+    if grad_z is not None:
+        grad_z = grad_z.detach().to(torch.float32).reshape(1).contiguous()
+    dx = torch.empty_like(x)
+    dweight = torch.empty_like(weight)
+    dgate = torch.empty((H, E), dtype=gate_w.dtype, device=dev)
+    nbytes = lib.moe_rmsnorm_router_bwd_workspace(N, H, E, K, xdt, wdt)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_rmsnorm_router_bwd(
+        x.data_ptr(), xdt, weight.data_ptr(), ndt, rstd.data_ptr(), xn.data_ptr(), gate_w.data_ptr(), wdt,
+        logits.data_ptr(), idx.data_ptr(), L.ptr(grad_w), gdt, L.ptr(cnt), L.ptr(grad_aux), L.ptr(grad_z),
+        float(aux_coef), float(z_coef), L.ptr(dxn), N, H, E, K, dx.data_ptr(), dweight.data_ptr(),
+        dgate.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+    )
+    L.check(rc, "moe_rmsnorm_router_bwd")
+    return dx, dweight, dgate
+
+
 # ---------------------------------------------------------------------------
 # Dispatch planner, permute, combine
 # ---------------------------------------------------------------------------

@@ -215,9 +215,19 @@ int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* 
  * first and the router kernels read xn.
  *
  * moe_rmsnorm_bwd: dx = rstd (g - xhat mean_h(g xhat)), xhat = x rstd,
- * g = gamma * (dxn + dxn2) (dxn2 optional: a second gradient of xn, e.g. the
- * router's, summed in fp32 inside the kernel); dgamma = sum_t (dxn + dxn2) xhat
- * in gamma's dtype, summed in a fixed order (deterministic).
+ * g = gamma * u, u = dxn + dxn2 (dxn2 optional: a second gradient of xn, e.g.
+ * the router's; the sum is rounded to x's dtype, as a sum of two gradients of
+ * xn is); dgamma = sum_t u xhat in gamma's dtype, summed in a fixed order
+ * (deterministic).
+ *
+ * moe_rmsnorm_router_bwd: the backward of moe_rmsnorm_router_fwd: the router
+ * backward of moe_router_bwd over xn (same grad_w / grad_aux / grad_z / cnt
+ * contract; dwg_out in wg's dtype) and the norm backward of dxn plus the
+ * router's gradient of xn (dxn may be null: no gradient from the expert path).
+ * For bf16 x and gate with E <= 16 and H % 256 == 0 the router's gradient of
+ * xn is formed inside the norm kernel from dL/dlogits and never reaches HBM;
+ * otherwise moe_router_bwd writes it to the workspace and moe_rmsnorm_bwd
+ * adds it.
  * ---------------------------------------------------------------------- */
 int moe_rmsnorm_fwd(const void* x, int x_dtype, const void* gamma, int gamma_dtype, float eps, int64_t N,
                     int64_t H, void* xn_out, float* rstd_out, void* stream);
@@ -232,6 +242,13 @@ size_t moe_rmsnorm_bwd_workspace(int64_t N, int64_t H);
 int moe_rmsnorm_bwd(const void* x, int x_dtype, const void* gamma, int gamma_dtype, const float* rstd,
                     const void* dxn, const void* dxn2, int64_t N, int64_t H, void* dx_out, void* dgamma_out,
                     void* workspace, size_t ws_bytes, void* stream);
+size_t moe_rmsnorm_router_bwd_workspace(int64_t N, int64_t H, int64_t E, int64_t K, int x_dtype, int wg_dtype);
+int moe_rmsnorm_router_bwd(const void* x, int x_dtype, const void* gamma, int gamma_dtype, const float* rstd,
+                           const void* xn, const void* wg, int wg_dtype, const float* logits, const int64_t* idx,
+                           const void* grad_w, int gw_dtype, const int64_t* cnt, const float* grad_aux,
+                           const float* grad_z, float aux_coef, float z_coef, const void* dxn, int64_t N, int64_t H,
+                           int64_t E, int64_t K, void* dx_out, void* dgamma_out, void* dwg_out, void* workspace,
+                           size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -74,7 +74,8 @@ def test_rmsnorm_backward_parity(shape, second):
     d = dev()
     _, rstd = ops.rmsnorm_forward(x.to(d), w.to(d), 1e-5)
     dx, dw = ops.rmsnorm_backward(x.to(d), w.to(d), rstd, dy.to(d), None if dy2 is None else dy2.to(d))
-    g = dy.double() + (dy2.double() if second else 0.0)
+    # the kernel's contract: the sum of two gradients of xn is rounded to x's dtype (as autograd's sum is)
+    g = (dy.float() + dy2.float()).to(xd).double() if second else dy.double()
     rdx, rdw = ON.rmsnorm_bwd(x, w, g, 1e-5)
     assert dx.dtype == xd and dw.dtype == wd
     # each gradient is computed in fp32 and rounded once to its own storage type
@@ -104,12 +105,13 @@ def test_rmsnorm_rejects_bad_shapes():
         ops.rmsnorm_forward(torch.zeros(4, 16384, device=d), torch.ones(16384, device=d), 1e-5)  # H > 8192
 
 
-# (N, H, E, K, dtype): the first four take the fused kernel, the rest the norm kernel + router kernels
+# (N, H, E, K, dtype): the first five take the fused forward kernel, the rest the norm kernel + router kernels
 ROUTE_SHAPES = [
     (16384, 4096, 8, 2, torch.bfloat16),   # C2 shape
     (1000, 2048, 16, 4, torch.bfloat16),   # E = 16
     (129, 512, 5, 2, torch.bfloat16),      # E < 8, ragged block
     (40, 256, 12, 12, torch.bfloat16),     # K == E
+    (200, 520, 8, 2, torch.bfloat16),      # H % 256 != 0: fused forward, backward through the router kernels
     (300, 2048, 64, 6, torch.bfloat16),    # E = 64: wide router kernel over xn
     (200, 512, 8, 2, torch.float32),       # fp32: generic router over xn
 ]
@@ -162,14 +164,15 @@ def test_norm_router_forward_parity(shape):
         assert torch.equal(xn.cpu(), xn2.cpu())
 
 
-@pytest.mark.parametrize("shape", [ROUTE_SHAPES[0], ROUTE_SHAPES[1], ROUTE_SHAPES[4]], ids=_rid)
-def test_norm_router_backward_parity(shape):
+@pytest.mark.parametrize("expert_grad", [True, False], ids=["with_dxn", "router_only"])
+@pytest.mark.parametrize("shape", ROUTE_SHAPES[:6], ids=_rid)
+def test_norm_router_backward_parity(shape, expert_grad):
     """NormRouterCore's gradients against the chain rule over the oracle: the router backward on xn (oracle
-    router_full with the kernel's routing), its dxn plus an expert-path gradient of xn, then the norm's
-    backward."""
+    router_full with the kernel's routing), its dxn plus an expert-path gradient of xn (or none), then the
+    norm's backward."""
     N, H, E, K, xd = shape
     N = min(N, 2048)
-    say(f"[norm router bwd] {_rid(shape)}")
+    say(f"[norm router bwd] {_rid(shape)} expert_grad={expert_grad}")
     x, nw, gw = _x(N, H, xd, N + 1), _w(H, torch.float32, H + 2), _gate(H, E, xd, E + 3)
     g = torch.Generator().manual_seed(N + 4)
     gwt = torch.randn(N, K, generator=g).to(xd)
@@ -177,7 +180,11 @@ def test_norm_router_backward_parity(shape):
     d = dev()
     xd_, nwd, gwd = x.to(d).requires_grad_(True), nw.to(d).requires_grad_(True), gw.to(d).requires_grad_(True)
     xn, idx, w, aux, z, logits, cnt, stats = NormRouterCore.apply(xd_, nwd, 1e-5, gwd, K, 0.01, 1e-3, None)
-    loss = (w.float() * gwt.to(d).float()).sum() + aux + z + (xn.float() * gxn.to(d).float()).sum()
+    if not expert_grad:
+        gxn = torch.zeros_like(gxn)
+    loss = (w.float() * gwt.to(d).float()).sum() + aux + z
+    if expert_grad:
+        loss = loss + (xn.float() * gxn.to(d).float()).sum()
     loss.backward()
     torch.cuda.synchronize()
     xn_c = xn.detach().cpu()
