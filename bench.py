@@ -332,12 +332,13 @@ def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=64, budget_s=15.0):
 def norm_router_bytes(N, H, E, K):
     """Algorithmic HBM bytes of the fused norm+router forward launch and of one fused fwd+bwd step.
 
-    Forward: read x, write xn, the router's per-token outputs (logits, lse, rstd, idx, w).  Backward: the
-    router backward reads xn and writes its dxn (two [N,H] passes), the norm backward reads x, the expert
-    path's dxn and the router's dxn and writes dx (four passes)."""
+    Forward: read x, write xn, the router's per-token outputs (logits, lse, rstd, idx, w).  Backward, counted
+    once: read x and the expert path's gradient of xn, write dx (three [N,H] passes), plus the saved logits,
+    top-k, upstream weight gradients, rstd, the gate and its gradient, gamma and its gradient.  (The kernels
+    re-read xn for the gate gradient: four passes.)"""
     tok = N * E * 4 + N * 4 + N * 4 + N * K * (8 + 2)
     fwd = 2 * N * H * 2 + H * E * 2 + H * 4 + tok
-    bwd = 6 * N * H * 2 + 2 * H * E * 2 + H * E * 4 + N * E * 4 + N * K * (8 + 2) + E * 8 + 2 * H * 4
+    bwd = 3 * N * H * 2 + 2 * H * E * 2 + N * E * 4 + N * K * (8 + 2) + N * 4 + E * 8 + 2 * H * 4
     return {"k_rmsnorm_route": fwd, "step": fwd + bwd}
 
 
@@ -386,7 +387,8 @@ def run_norm_router(args, torch):
     return {
         "workload": "C2 RMSNorm + router fwd+bwd (norm fused into the router read)", "tokens": N, "d_model": H,
         "experts": E, "top_k": K, "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
-        "fwd_bwd_GBps": round(alg["step"] / (ms * 1e-3) / 1e9, 1), "graph_ms_per_step": gms,
+        "fwd_bwd_GBps": round(alg["step"] / (ms * 1e-3) / 1e9, 1),
+        "fwd_bwd_frac_of_hbm_peak": round(alg["step"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "graph_ms_per_step": gms,
         "unfused_ms_per_step": ms_comp, "torch_norm_ms_per_step": ms_torch,
         "alg_bytes_per_step": alg["step"],
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -306,13 +306,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(NormFwdArgs a) {
   const int N = a.N, H = a.H;
   const TX* __restrict__ x = static_cast<const TX*>(a.x);
   TX* __restrict__ xn = static_cast<TX*>(a.xn);
-  stage_gamma<TG, NCH>(s_gam, static_cast<const TG*>(a.gamma), H, tid, 256);
-  __syncthreads();
   const int rowbytes = H * (int)sizeof(TX);
   const int nwt = gridDim.x * 4;
   int t = blockIdx.x * 4 + wv;
-  RowFrag<TX, NCH> f;
+  RowFrag<TX, NCH> f;  // the first row is requested before the LDS staging, whose latency it then overlaps
   if (t < N) frag_load_all(f, buf_rsrc(x + (int64_t)t * H, rowbytes), lane);
+  stage_gamma<TG, NCH>(s_gam, static_cast<const TG*>(a.gamma), H, tid, 256);
+  __syncthreads();
   for (; t < N; t += nwt) {
     row_fence();
     const int tn = t + nwt;
@@ -336,22 +336,25 @@ __global__ __launch_bounds__(256) void k_rmsnorm_fwd(NormFwdArgs a) {
   }
 }
 
-// Forward with the router fused in (bf16 x and gate, E <= EP in {8, 16}).  Block = 8 waves (one per CU: the
-// gate image fills most of the LDS); each wave takes two rows at a time, t0 and t1 = t0 + stride, so one
-// LDS read of the gate serves both rows' dot products and one reduce-scatter + routing pass serves both
-// tokens (lanes 0-31 route t0, lanes 32-63 route t1, each in its first 16-lane row).
-constexpr int kRouteWaves = 8;
-template <int NCH, int EP>
+// Forward with the router fused in (bf16 x and gate, E <= EP in {8, 16}).  One block per CU (the gate image
+// fills most of the LDS).  Each wave takes R rows at a time, t_r = t0 + r * stride: one LDS read of the gate
+// serves all R rows' dot products and one reduce-scatter + routing pass serves all R tokens (token r is
+// routed by lanes 32 r .. 32 r + 31 for R = 2, by all lanes for R = 1, in the first 16-lane row of those).
+// R = 2 with 8 waves a block, R = 1 with 16 (half the row registers, twice the waves).
+template <int R>
+constexpr int route_waves() { return R == 2 ? 8 : 16; }
+template <int NCH, int EP, int R>
 constexpr size_t norm_route_lds() {
+  constexpr int NWV = route_waves<R>();
   return (size_t)NCH * 2048 + (size_t)EP * NCH * 1024 +
-         (EP + kRouteWaves * EP + 2 * kRouteWaves + 4 + finalize_scratch_floats<kRouteWaves * 64>()) * 4;
+         (EP + NWV * EP + 2 * NWV + 4 + finalize_scratch_floats<NWV * 64>()) * 4;
 }
 
-template <typename TG, int NCH, int EP>
-__global__ __launch_bounds__(kRouteWaves * 64) void k_rmsnorm_route(NormFwdArgs a) {
-  constexpr int NWV = kRouteWaves;
+template <typename TG, int NCH, int EP, int R>
+__global__ __launch_bounds__(route_waves<R>() * 64) void k_rmsnorm_route(NormFwdArgs a) {
+  constexpr int NWV = route_waves<R>();
   constexpr int NT = NWV * 64;
-  constexpr int NV = 2 * EP;  // (token, expert) partial sums of a lane
+  constexpr int NV = R * EP;  // (token, expert) partial sums of a lane
   extern __shared__ __attribute__((aligned(16))) uint8_t nsm[];
   f32x4* s_gam = reinterpret_cast<f32x4*>(nsm);             // [NCH * 2][64]
   u32x4* s_w = reinterpret_cast<u32x4*>(nsm + NCH * 2048);  // [EP / 4][NCH * 4][64]
@@ -368,79 +371,76 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_rmsnorm_route(NormFwdArgs 
   const int N = a.N, H = a.H, E = a.E, K = a.K;
   const uint16_t* __restrict__ x = static_cast<const uint16_t*>(a.x);
   uint16_t* __restrict__ xn = static_cast<uint16_t*>(a.xn);
+  const int rowbytes = H * 2;
+  const int nwt = gridDim.x * NWV;
+  auto rows = [&](int t) { return buf_rsrc(x + (int64_t)t * H, t < N ? rowbytes : 0); };
+  int t0 = blockIdx.x * NWV + wv;
+  RowFrag<uint16_t, NCH> f[R];  // the first rows are requested before the LDS staging (their latencies overlap)
+  if (t0 < N) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) frag_load_all(f[r], rows(t0 + r * nwt), lane);
+  }
   stage_gamma<TG, NCH>(s_gam, static_cast<const TG*>(a.gamma), H, tid, NT);
   stage_gate_fwd<NCH, EP>(s_w, a.wg, H, E, tid, NT);
   if (tid < EP) s_cnt[tid] = 0;
   __syncthreads();
 
-  const int el = lane & 15;                    // expert of this lane inside its 16-lane row
-  const int tr = lane >> 5;                    // token of the pair this lane routes
-  const bool lead = (lane & 16) == 0;          // the 16-lane row whose results are stored
+  const int el = lane & 15;                           // expert of this lane inside its 16-lane row
+  const int tr = R == 2 ? lane >> 5 : 0;              // token this lane routes
+  const bool lead = (lane & (R == 2 ? 16 : 48)) == 0;  // the 16-lane row whose results are stored
   const bool real = el < E;
   const bool has_bias = a.bias != nullptr;
   const float bias_v = (has_bias && real) ? a.bias[el] : 0.f;
   float pacc = 0.f, zacc = 0.f;
   int nfacc = 0;
 
-  const int rowbytes = H * 2;
-  const int nwt = gridDim.x * NWV;
-  auto rows = [&](int t) { return buf_rsrc(x + (int64_t)t * H, t < N ? rowbytes : 0); };
-  int t0 = blockIdx.x * NWV + wv;
-  RowFrag<uint16_t, NCH> f0, f1;
-  if (t0 < N) {
-    frag_load_all(f0, rows(t0), lane);
-    frag_load_all(f1, rows(t0 + nwt), lane);
-  }
-  for (; t0 < N; t0 += 2 * nwt) {
+  for (; t0 < N; t0 += R * nwt) {
     row_fence();
-    const int t1 = t0 + nwt;
-    const bool v1 = t1 < N;
-    const buf_rsrc_t rn0 = rows(t0 + 2 * nwt), rn1 = rows(t1 + 2 * nwt);
-    const float r0 = rsqrtf(frag_sumsq(f0) / (float)H + a.eps);
-    const float r1 = rsqrtf(frag_sumsq(f1) / (float)H + a.eps);
-    if (lane == 0) {
-      a.rstd[t0] = r0;
-      if (v1) a.rstd[t1] = r1;
+    buf_rsrc_t rn[R];
+    float rs[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int tr_ = t0 + r * nwt;
+      rn[r] = rows(tr_ + R * nwt);
+      rs[r] = rsqrtf(frag_sumsq(f[r]) / (float)H + a.eps);
+      if (lane == 0 && tr_ < N) a.rstd[tr_] = rs[r];
     }
     float acc[NV];
 #pragma unroll
     for (int e = 0; e < NV; ++e) acc[e] = 0.f;
-    uint16_t* orow0 = xn + (int64_t)t0 * H;
-    uint16_t* orow1 = xn + (int64_t)t1 * H;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       float v[8], g[8], o[8];
-      u32x4 pk0, pk1;
+      u32x4 pk[R];
       const int c = lane + 64 * j;
       gamma_get<NCH>(s_gam, j, lane, g);
-      frag_get(f0, j, v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (v[i] * r0) * g[i];
-      chunk_store<uint16_t>(orow0, c, 8 * c < H, o, pk0);
-      frag_get(f1, j, v);
+      for (int r = 0; r < R; ++r) {
+        const int tr_ = t0 + r * nwt;
+        frag_get(f[r], j, v);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (v[i] * r1) * g[i];
-      chunk_store<uint16_t>(orow1, c, v1 && 8 * c < H, o, pk1);
+        for (int i = 0; i < 8; ++i) o[i] = (v[i] * rs[r]) * g[i];
+        chunk_store<uint16_t>(xn + (int64_t)tr_ * H, c, tr_ < N && 8 * c < H, o, pk[r]);
+      }
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int q = 0; q < EP / 4; ++q) {
           const u32x4 wq = s_w[((q * NCH + j) * 4 + m) * 64 + lane];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            acc[4 * q + k] = dot2bf(pk0[m], wq[k], acc[4 * q + k]);
-            acc[EP + 4 * q + k] = dot2bf(pk1[m], wq[k], acc[EP + 4 * q + k]);
-          }
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r * EP + 4 * q + k] = dot2bf(pk[r][m], wq[k], acc[r * EP + 4 * q + k]);
         }
-      frag_load(f0, rn0, j, lane);  // the next pair's chunk j into the registers just freed
-      frag_load(f1, rn1, j, lane);
+#pragma unroll
+      for (int r = 0; r < R; ++r) frag_load(f[r], rn[r], j, lane);  // the next rows' chunk j into the freed registers
       chunk_fence(acc);
     }
     // ---- logits: the wave total of (token, expert) i ends in lanes i * (64 / NV) ..; gather token tr's
     // expert el to lane el of the token's 16-lane rows ----
     const float tot = wave_reduce_scatter<NV>(acc, lane);
     float lg = __shfl(tot, (tr * EP + (el < EP ? el : 0)) * (64 / NV));
-    const int t = tr ? t1 : t0;
+    const int t = t0 + tr * nwt;
     const bool vt = t < N;
     if (has_bias) lg += bias_v;
     if (lead && real && vt) a.logits[(int64_t)t * E + el] = lg;
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_rmsnorm_route(NormFwdArgs 
     const float s = row16_sum(ex);
     const float inv = 1.f / s;
     const float lse = m + logf(s);
-    if ((lane & 31) == 0 && vt) a.lse[t] = lse;
+    if (lead && el == 0 && vt) a.lse[t] = lse;
     zacc += vt ? lse * lse : 0.f;
     pacc += vt ? ex * inv : 0.f;
     // top-k: K rounds of arg-max (larger logit, lower id on a tie) over the experts not taken yet
@@ -475,9 +475,10 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_rmsnorm_route(NormFwdArgs 
       atomicAdd(&s_cnt[my_e], 1);
     }
   }
-  // the two tokens' accumulators (lanes l and l + 32) in a fixed order
-  pacc += __shfl_xor(pacc, 32);
-  zacc += __shfl_xor(zacc, 32);
+  if constexpr (R == 2) {  // the two tokens' accumulators (lanes l and l + 32) in a fixed order
+    pacc += __shfl_xor(pacc, 32);
+    zacc += __shfl_xor(zacc, 32);
+  }
   if (lane < EP) s_p[wv][lane] = pacc;
   if (lane == 0) {
     s_z[wv] = zacc;
@@ -536,12 +537,18 @@ struct NormBwdArgs {
 template <int NCH, int MODE>
 constexpr size_t norm_bwd_lds() { return (size_t)NCH * 4096 + (MODE >= 8 ? (size_t)MODE * NCH * 1024 : 0); }
 
-// Two waves per SIMD up to H = 4096 (the row state is about 160 VGPRs there); wider rows take one.
+// Two waves per SIMD up to H = 4096 (the row state takes about 256 VGPRs there); wider rows take one.  With
+// the gate image in LDS (MODE 8 / 16) one block fills a CU's LDS, so those blocks have eight waves.
+template <int MODE>
+constexpr int norm_bwd_waves() { return MODE >= 8 ? 8 : 4; }
+
 template <typename TX, typename TG, int NCH, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCH <= 8 ? 2 : 1))) void k_rmsnorm_bwd(
-    NormBwdArgs a) {
+__global__ __launch_bounds__(norm_bwd_waves<MODE>() * 64) __attribute__((amdgpu_waves_per_eu(NCH <= 8 ? 2 : 1)))
+void k_rmsnorm_bwd(NormBwdArgs a) {
   constexpr bool TWO = MODE == 1;
   constexpr int EP = MODE >= 8 ? MODE : 0;
+  constexpr int NWV = norm_bwd_waves<MODE>();
+  constexpr int NT = NWV * 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t nsm[];
   f32x4* s_gam = reinterpret_cast<f32x4*>(nsm);             // [NCH * 2][64]
   f32x4* s_dg = s_gam + NCH * 128;                           // [NCH * 2][64]
@@ -554,9 +561,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCH <= 8 ? 
   const TX* __restrict__ dxn = static_cast<const TX*>(a.dxn);
   const TX* __restrict__ dxn2 = static_cast<const TX*>(a.dxn2);
   TX* __restrict__ dx = static_cast<TX*>(a.dx);
-  stage_gamma<TG, NCH>(s_gam, static_cast<const TG*>(a.gamma), H, tid, 256);
+  const int rowbytes = H * (int)sizeof(TX);
+  const int nwt = gridDim.x * NWV;
+  int t = blockIdx.x * NWV + wv;
+  // a null gradient (or a row past N) reads as zeros through a descriptor with no records
+  auto rows = [&](const TX* base, int row) {
+    return buf_rsrc(base ? base + (int64_t)row * H : x, (base && row < N) ? rowbytes : 0);
+  };
+  RowFrag<TX, NCH> fx, fg, fg2;  // the first row is requested before the LDS staging (latencies overlap)
+  if (t < N) {
+    frag_load_all(fx, rows(x, t), lane);
+    frag_load_all(fg, rows(dxn, t), lane);
+    if constexpr (TWO) frag_load_all(fg2, rows(dxn2, t), lane);
+  }
+  stage_gamma<TG, NCH>(s_gam, static_cast<const TG*>(a.gamma), H, tid, NT);
   if constexpr (EP > 0)
-    stage_gate_bwd<NCH, EP>(s_w, a.wg, H, a.E, tid, 256);
+    stage_gate_bwd<NCH, EP>(s_w, a.wg, H, a.E, tid, NT);
   __syncthreads();
 
   float dg[NCH][8];
@@ -564,19 +584,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCH <= 8 ? 
   for (int j = 0; j < NCH; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) dg[j][i] = 0.f;
-  const int rowbytes = H * (int)sizeof(TX);
-  const int nwt = gridDim.x * 4;
-  int t = blockIdx.x * 4 + wv;
-  // a null gradient (or a row past N) reads as zeros through a descriptor with no records
-  auto rows = [&](const TX* base, int row) {
-    return buf_rsrc(base ? base + (int64_t)row * H : x, (base && row < N) ? rowbytes : 0);
-  };
-  RowFrag<TX, NCH> fx, fg, fg2;
-  if (t < N) {
-    frag_load_all(fx, rows(x, t), lane);
-    frag_load_all(fg, rows(dxn, t), lane);
-    if constexpr (TWO) frag_load_all(fg2, rows(dxn2, t), lane);
-  }
   for (; t < N; t += nwt) {
     row_fence();
     const int tn = t + nwt;
@@ -655,9 +662,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCH <= 8 ? 
       chunk_fence();
     }
   }
-  // dgamma: the block's four waves summed in order in LDS, one partial row per block
+  // dgamma: the block's waves summed in order in LDS, one partial row per block
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < NWV; ++w) {
     if (wv == w) {
 #pragma unroll
       for (int j = 0; j < NCH; ++j)
@@ -670,7 +677,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCH <= 8 ? 
     }
     __syncthreads();
   }
-  for (int i = tid; i < NCH * 128; i += 256) {
+  for (int i = tid; i < NCH * 128; i += NT) {
     const int l = i & 63, q = (i >> 6) & 1, j = i >> 7;
     const int h0 = 8 * (l + 64 * j) + 4 * q;
     if (h0 < H) *reinterpret_cast<f32x4*>(a.part_dg + (int64_t)blockIdx.x * H + h0) = s_dg[i];
@@ -713,9 +720,15 @@ namespace {
 int norm_nch(int64_t H) { return H <= 512 ? 1 : H <= 2048 ? 4 : H <= 4096 ? 8 : 16; }
 int norm_fwd_blocks(int64_t N) { return (int)std::min<int64_t>(1024, std::max<int64_t>(1, (N + 3) / 4)); }
 // one block of eight waves per CU; one partial set per block for the statistics fold
-int norm_route_blocks(int64_t N) { return (int)std::min<int64_t>(256, std::max<int64_t>(1, (N + 7) / 8)); }
+constexpr int kRouteRows = 1;  // one row per wave, 16 waves a block (slightly ahead of two rows, 8 waves)
+int norm_route_blocks(int64_t N) {
+  constexpr int nw = route_waves<kRouteRows>() * kRouteRows;
+  return (int)std::min<int64_t>(256, std::max<int64_t>(1, (N + nw - 1) / nw));
+}
 // the backward writes one dgamma partial row per block: about two blocks per CU
 int norm_bwd_blocks(int64_t N) { return (int)std::min<int64_t>(512, std::max<int64_t>(1, (N + 3) / 4)); }
+// the fused backward: one block of eight waves per CU
+int norm_route_bwd_blocks(int64_t N) { return (int)std::min<int64_t>(256, std::max<int64_t>(1, (N + 7) / 8)); }
 int norm_route_ep(int64_t E) { return E <= 8 ? 8 : 16; }
 size_t align256n(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -737,7 +750,7 @@ size_t align256n(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t route_lds(int nch, int ep) {
   size_t b = 0;
-  MOE_NCH(nch, b = (ep == 8 ? norm_route_lds<NCHv, 8>() : norm_route_lds<NCHv, 16>()));
+  MOE_NCH(nch, b = (ep == 8 ? norm_route_lds<NCHv, 8, kRouteRows>() : norm_route_lds<NCHv, 16, kRouteRows>()));
   return b;
 }
 size_t route_bwd_lds(int nch, int ep) {
@@ -786,9 +799,10 @@ int launch_norm_fwd(int nblk, hipStream_t s, const NormFwdArgs& a) {
 
 template <typename TG, int NCH, int EP>
 int launch_norm_route(int nblk, hipStream_t s, const NormFwdArgs& a) {
-  constexpr size_t lds = norm_route_lds<NCH, EP>();
-  if (int rc = allow_lds(k_rmsnorm_route<TG, NCH, EP>, lds)) return rc;
-  MOE_LAUNCH("k_rmsnorm_route", (k_rmsnorm_route<TG, NCH, EP>), dim3(nblk), dim3(kRouteWaves * 64), lds, s, a);
+  constexpr size_t lds = norm_route_lds<NCH, EP, kRouteRows>();
+  if (int rc = allow_lds(k_rmsnorm_route<TG, NCH, EP, kRouteRows>, lds)) return rc;
+  MOE_LAUNCH("k_rmsnorm_route", (k_rmsnorm_route<TG, NCH, EP, kRouteRows>), dim3(nblk),
+             dim3(route_waves<kRouteRows>() * 64), lds, s, a);
   return check_launch("k_rmsnorm_route");
 }
 
@@ -797,7 +811,7 @@ int launch_norm_bwd(int nblk, hipStream_t s, const NormBwdArgs& a) {
   constexpr size_t lds = norm_bwd_lds<NCH, MODE>();
   constexpr const char* name = MODE >= 8 ? "k_rmsnorm_route_bwd" : "k_rmsnorm_bwd";
   if (int rc = allow_lds(k_rmsnorm_bwd<TX, TG, NCH, MODE>, lds)) return rc;
-  MOE_LAUNCH(name, (k_rmsnorm_bwd<TX, TG, NCH, MODE>), dim3(nblk), dim3(256), lds, s, a);
+  MOE_LAUNCH(name, (k_rmsnorm_bwd<TX, TG, NCH, MODE>), dim3(nblk), dim3(norm_bwd_waves<MODE>() * 64), lds, s, a);
   return check_launch(name);
 }
 
@@ -959,7 +973,7 @@ NormRouteBwdPlan plan_norm_route_bwd(int64_t N, int64_t H, int64_t E, int64_t K,
   p.fused = x_dt == MOE_BF16 && wg_dt == MOE_BF16 && norm_route_bwd_fits(H, E);
   p.nch = norm_nch(H);
   p.ep = norm_route_ep(E);
-  p.nblk = norm_bwd_blocks(N);
+  p.nblk = p.fused ? norm_route_bwd_blocks(N) : norm_bwd_blocks(N);
   if (p.fused) {
     p.off_g = 0;
     p.off_rw = align256n((size_t)N * p.ep * 2);
