@@ -9,11 +9,12 @@ timing starts; ``moe_mi355/configs.py``):
   layer   C4 (headline): full MoE layer fwd+bwd, T=8192 d=4096 E=8 SwiGLU
           F=14336 K=2, bf16 -- router, planner, permute, grouped gate/up/down
           GEMM, combine, and the whole backward.  ``value`` = tokens/s.
-  router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2 (always measured too,
-          reported under "router").
+  router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2 (measured with the
+          layer too, reported under "router").
   norm_router  C2 shape with the block's RMSNorm in front of the router:
           the norm fused into the router's read of the hidden state, fwd+bwd,
-          beside the unfused composition and a torch-ops norm.
+          beside the unfused composition and a torch-ops norm (measured with
+          the layer too, under "norm_router").
   dispatch C3: router + planner + permute + combine forward, T=65536 d=2048
           E=64 K=6, cf=1.25 with drops.
   skewed  C5: layer fwd+bwd, T=32768 d=2048 E=128 F=768 K=8, cf=1.0 drops,
@@ -466,6 +467,8 @@ def main():
         log(f"[bench] layer: {main_res['ms_per_step']:.3f} ms/step")
         extra["router"] = run_router(args, torch)
         log(f"[bench] router: {extra['router']['ms_per_step']:.4f} ms/step")
+        extra["norm_router"] = run_norm_router(args, torch)
+        log(f"[bench] norm_router: {extra['norm_router']['ms_per_step']:.4f} ms/step")
         cpu = None if args.no_cpu_baseline else cpu_baseline_layer(torch, configs.C4, args.layout, inp)
         del inp
         if not args.no_cpu_baseline:
@@ -500,7 +503,6 @@ def main():
         roof = main_res.pop("roofline")
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
     if args.workload == "all":
-        extra["norm_router"] = run_norm_router(args, torch)
         extra["dispatch"] = run_dispatch(args, torch)
         extra["skewed"] = run_layer(args, torch, configs.C5, "routed", configs.layer_inputs(configs.C5))
     main_res.pop("ms_per_step", None)
