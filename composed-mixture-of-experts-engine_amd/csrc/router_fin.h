@@ -1,6 +1,6 @@
 // Router statistics finalize shared by the router kernels: per-block partials (dispatch counts,
 // probability sums, z sums, non-finite counts) written through to the coherence point, and the fixed-order
-// fold of all of them into cnt / stats / aux / z by one block.
+// fold of all of them into cnt / stats / aux / z by one block (stats[7]: experts that received no token).
 #pragma once
 
 #include "common.h"
@@ -169,14 +169,17 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
   __syncthreads();
   if (tid < 64) {  // wave 0: the per-expert statistics in double, lane-strided then a fixed butterfly
     double tot = 0.0, mx = 0.0, aux = 0.0;
+    int dead = 0;
     for (int e = tid; e < E; e += 64) {
       const double c = s_c[e];
       tot += c;
       mx = fmax(mx, c);
       aux += (c / ((double)N * K)) * (double)s_pe[e];
+      dead += c == 0.0;
     }
     tot = wave_sum(tot);
     aux = wave_sum(aux);
+    dead = wave_sum(dead);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
     const double mean = tot / E;
@@ -199,7 +202,7 @@ __device__ __forceinline__ void router_finalize_block(const int* __restrict__ pa
     stats[4] = E > 1 ? (float)sqrt(var / (E - 1)) : NAN;
     stats[5] = (float)tot;
     stats[6] = nf;
-    stats[7] = 0.f;
+    stats[7] = (float)dead;
     if (aux_out) aux_out[0] = aux_coef * aux_raw;
     if (z_out) z_out[0] = z_coef * zstat;
   }

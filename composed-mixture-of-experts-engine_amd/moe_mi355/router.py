@@ -31,6 +31,7 @@ STAT_CNT_MEAN = 3
 STAT_CNT_STD = 4
 STAT_CNT_TOTAL = 5
 STAT_NONFINITE = 6
+STAT_DEAD = 7
 
 
 class RouterCore(torch.autograd.Function):

@@ -188,6 +188,7 @@ class MoERouter(torch.nn.Module):
         self.last_z_loss: Optional[torch.Tensor] = None
         self.last_stats: Optional[torch.Tensor] = None
         self.last_stats_host: Optional[torch.Tensor] = None
+        self.last_num_tokens = 0
         # Fixed (non-learnable) additive logit bias [E] f32, e.g. a load-skew
         # harness; unlike ``bias`` it keeps w differentiable.  None = off.
         self.register_buffer("logit_bias", None)
@@ -239,6 +240,7 @@ class MoERouter(torch.nn.Module):
         self.last_aux_loss = aux
         self.last_z_loss = z
         self.last_stats = stats
+        self.last_num_tokens = N
 
         if self.sync_profile:
             head = stats[:8].to("cpu")  # the single device->host copy of this forward

@@ -44,7 +44,7 @@ enum moe_status {
  *   [4] cnt_std     unbiased standard deviation of cnt
  *   [5] cnt_total   sum(cnt)  (== N*K when every slot was dispatched)
  *   [6] nonfinite   number of non-finite logits
- *   [7] reserved
+ *   [7] dead        number of experts with cnt == 0
  *   [8 + e]         mean_t p[t,e]
  */
 #define MOE_STATS_HEAD 8
@@ -249,6 +249,28 @@ int moe_rmsnorm_router_bwd(const void* x, int x_dtype, const void* gamma, int ga
                            const float* grad_z, float aux_coef, float z_coef, const void* dxn, int64_t N, int64_t H,
                            int64_t E, int64_t K, void* dx_out, void* dgamma_out, void* dwg_out, void* workspace,
                            size_t ws_bytes, void* stream);
+
+/* ----------------------------------------------------------------------
+ * Per-step routing telemetry on the device: replaces the host-side routing
+ * block of the reference's train step (moe-engine/train.py L:360-399, which
+ * reads the RouterProfile of moe_router.py L:594-612 / L:690-745 and the
+ * dispatch counts with .item() synchronisations every step).
+ *
+ * moe_telemetry_record writes one record of moe_telemetry_fields() floats
+ * (16) at `record` (e.g. one slot of a ring buffer) from the router's stats
+ * vector (stats_out of moe_router_fwd / moe_rmsnorm_router_fwd, same stream)
+ * and, optionally, the planner's drop count (ndrop of moe_plan; null = no
+ * capacity drops):
+ *   [0] step  [1] load imbalance  [2] z statistic  [3] tokens/expert mean
+ *   [4] tokens/expert std  [5] dead experts  [6] active experts
+ *   [7] routing efficiency = dispatched / (capacity_factor * N * K)
+ *   [8] dropped fraction = ndrop / (N * K)  [9] aux statistic
+ *   [10] non-finite logits  [11] dispatched slots  [12..15] zero
+ * No host synchronisation; the caller copies its records when it logs.
+ * ---------------------------------------------------------------------- */
+int moe_telemetry_fields(void);
+int moe_telemetry_record(const float* stats, int64_t E, int64_t N, int64_t K, float capacity_factor,
+                         const int32_t* ndrop, int64_t step, float* record, void* stream);
 
 #ifdef __cplusplus
 }
