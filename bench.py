@@ -19,6 +19,8 @@ timing starts; ``moe_mi355/configs.py``):
           E=64 K=6, cf=1.25 with drops.
   skewed  C5: layer fwd+bwd, T=32768 d=2048 E=128 F=768 K=8, cf=1.0 drops,
           aux+z losses, Zipf(1.1) gate bias, routed layout.
+  fp8_fwd C4 layer forward without autograd, bf16 beside the e4m3 dispatch
+          payload + fp8 expert GEMMs (the fp8 line's dtype is "fp8-e4m3").
 
 One step = one forward + backward (forward only for dispatch).  W untimed
 warmup steps, then exactly K steps bracketed by torch.cuda.synchronize();
@@ -305,6 +307,57 @@ def run_layer(args, torch, cfg, layout, inp):
     return res
 
 
+MFMA_FP8_PEAK_TFLOPS = 5000.0
+
+
+def run_fp8_fwd(args, torch, inp):
+    """C4 layer forward (no autograd) in bf16 and with the e4m3 dispatch payload and fp8 expert GEMMs
+    (weights quantized once, outside the timed region, as an inference deployment keeps them)."""
+    cfg = configs_mod().C4
+    layer = build_layer(cfg, torch, inp, "reference")
+    x = inp["x"].to(torch.device("cuda:0"))
+    layer.quantize_fp8()
+
+    def bf16_step():
+        with torch.no_grad():
+            layer(x)
+
+    def fp8_step():
+        layer.forward_fp8(x)
+
+    log("[bench] timing C4 forward bf16 / fp8")
+    ms_bf16, prof_bf16 = timed(torch, bf16_step, args.steps, args.warmup, prof_steps=min(args.steps, 5))
+    ms_fp8, prof_fp8 = timed(torch, fp8_step, args.steps, args.warmup, prof_steps=min(args.steps, 5))
+    R = int(layer.last_plan.offsets[-1].item())
+    fl = gemm_flops(R, cfg.H, cfg.F)
+    fl8 = {"k_gemm_swiglu_fwd1_fp8": fl["k_gemm_swiglu_fwd1"], "k_gemm_swiglu_fwd2_fp8": fl["k_gemm_swiglu_fwd2"]}
+    k16 = kernel_table(prof_bf16, fl, 1e12, "TFLOPs")
+    k8 = kernel_table(prof_fp8, fl8, 1e12, "TFLOPs")
+    dom = "k_gemm_swiglu_fwd1_fp8"
+    fwd_flops = fl["k_gemm_swiglu_fwd1"] + fl["k_gemm_swiglu_fwd2"]
+    res = {
+        "workload": "C4 layer forward, bf16 vs e4m3 payload + fp8 expert GEMMs (no autograd)",
+        "tokens": cfg.T, "rows_computed": R,
+        "bf16_ms_per_step": ms_bf16, "bf16_tokens_per_s": cfg.T / (ms_bf16 * 1e-3),
+        "fp8_ms_per_step": ms_fp8, "fp8_tokens_per_s": cfg.T / (ms_fp8 * 1e-3),
+        "fp8_speedup": round(ms_bf16 / ms_fp8, 3),
+        "expert_TFLOP_per_step": fwd_flops / 1e12,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": k8[dom]["TFLOPs"], "peak": MFMA_FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(k8[dom]["TFLOPs"] / MFMA_FP8_PEAK_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": fl8[dom], "avg_us": k8[dom]["avg_us"]},
+        "kernels_bf16": k16, "kernels_fp8": k8,
+    }
+    del layer
+    torch.cuda.empty_cache()
+    return res
+
+
+def configs_mod():
+    from moe_mi355 import configs
+
+    return configs
+
+
 def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=64, budget_s=15.0):
     """float64 oracle layer fwd+bwd on the first ``sample_T`` tokens with the full-size weights."""
     from oracle import layer as OL
@@ -438,7 +491,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="layer", choices=["layer", "router", "norm_router", "dispatch", "skewed", "all"])
+    ap.add_argument("--workload", default="layer", choices=["layer", "router", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
     ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -489,6 +542,12 @@ def main():
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "top_k")}
+    elif args.workload == "fp8_fwd":
+        main_res = run_fp8_fwd(args, torch, configs.layer_inputs(configs.C4))
+        cpu = None
+        value, unit, ms = main_res["fp8_tokens_per_s"], "tokens/s", main_res["fp8_ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {"workload": main_res.pop("workload"), "tokens": main_res.pop("tokens")}
     elif args.workload == "dispatch":
         main_res = run_dispatch(args, torch)
         cpu = None
@@ -509,7 +568,8 @@ def main():
     main_res.pop("tokens_per_s", None)
     out = {
         "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3" if args.workload == "fp8_fwd" else "bf16",
         "data": "synthetic (seeded randn of the BASELINE config shapes; random-init weights)", "config": config,
         "roofline": roof, "cpu_baseline": cpu,
     }

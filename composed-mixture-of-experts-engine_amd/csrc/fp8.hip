@@ -1,0 +1,192 @@
+// e4m3 (OCP fp8) payloads of the expert FFN forward.
+//
+// Each row gets one fp32 scale, absmax / 448 (448 is the largest e4m3 value; an all-zero row gets 1), and
+// its elements are multiplied by inv = 448 / absmax (one division per row; 1 for a zero row) in fp32 and
+// rounded to nearest even by v_cvt_pk_fp8_f32.
+//
+// k_permute_fp8     the dispatch payload: row r of the permuted buffer is the quantized row of token
+//                   row_slot[r] / K (the rows k_permute copies), written at one byte per element -- half
+//                   the bytes of the bf16 permute -- with its scale in sx[r].
+// k_quant_rows_fp8  any [rows, cols] matrix (the expert weights once, the SwiGLU activations per forward).
+//
+// One wave per row: pass 1 takes the row's absmax, pass 2 quantizes 8 elements per lane and stores them as
+// one 8-byte word.  bf16 rows of up to 16K elements stay in registers between the passes (one read of the
+// row from memory); longer rows and fp32 rows are read twice.
+#include "common.h"
+
+namespace moe {
+
+constexpr float kE4M3Max = 448.f;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ void q_load8(const T* p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void q_load8<uint16_t>(const uint16_t* p, float (&v)[8]) {
+  const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    v[2 * m] = __uint_as_float(a[m] << 16);
+    v[2 * m + 1] = __uint_as_float(a[m] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void q_load8<float>(const float* p, float (&v)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    v[m] = a[m];
+    v[4 + m] = b[m];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void quant_row(const T* __restrict__ src, int cols, uint8_t* __restrict__ dst,
+                                          float* __restrict__ scale, int lane) {
+  float amax = 0.f;
+  for (int c = lane * 8; c < cols; c += 512) {
+    float v[8];
+    q_load8<T>(src + c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = wave_max(amax);
+  const float sc = amax > 0.f ? amax / kE4M3Max : 1.f;
+  const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+  if (lane == 0) *scale = sc;
+  for (int c = lane * 8; c < cols; c += 512) {
+    float v[8];
+    q_load8<T>(src + c, v);
+    uint32_t lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+    __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(dst + c));
+  }
+}
+
+// The same in one pass over memory for rows of at most 512 * NCH elements: the row is held in registers
+// (NCH 16-byte words of bf16 per lane) between the absmax and the quantization.
+template <int NCH>
+__device__ __forceinline__ void quant_row_reg(const uint16_t* __restrict__ src, int cols, uint8_t* __restrict__ dst,
+                                              float* __restrict__ scale, int lane) {
+  u32x4 w[NCH];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane * 8 + 512 * j;
+    w[j] = c < cols ? *reinterpret_cast<const u32x4*>(src + c) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(w[j][m] << 16)), fabsf(__uint_as_float(w[j][m] & 0xffff0000u))));
+  }
+  amax = wave_max(amax);
+  const float sc = amax > 0.f ? amax / kE4M3Max : 1.f;
+  const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+  if (lane == 0) *scale = sc;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = lane * 8 + 512 * j;
+    float v[8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      v[2 * m] = __uint_as_float(w[j][m] << 16);
+      v[2 * m + 1] = __uint_as_float(w[j][m] & 0xffff0000u);
+    }
+    uint32_t lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+    if (c < cols) __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(dst + c));
+  }
+}
+
+__device__ __forceinline__ int q_wave() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+template <int NCH>
+__global__ __launch_bounds__(256) void k_quant_rows_fp8_reg(const uint16_t* __restrict__ src, int64_t rows, int cols,
+                                                           int64_t ld, uint8_t* __restrict__ dst,
+                                                           float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + q_wave(); r < rows; r += (int64_t)gridDim.x * 4)
+    quant_row_reg<NCH>(src + r * ld, cols, dst + r * cols, scale + r, lane);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_quant_rows_fp8(const T* __restrict__ src, int64_t rows, int cols, int64_t ld,
+                                                       uint8_t* __restrict__ dst, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + q_wave(); r < rows; r += (int64_t)gridDim.x * 4)
+    quant_row<T>(src + r * ld, cols, dst + r * cols, scale + r, lane);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_permute_fp8(const T* __restrict__ x, const int* __restrict__ row_slot,
+                                                    const int* __restrict__ offsets, int E, int K, int H, int64_t R,
+                                                    uint8_t* __restrict__ xq, float* __restrict__ sx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = min(R, (int64_t)offsets[E]);
+  for (int64_t r = (int64_t)blockIdx.x * 4 + q_wave(); r < rows; r += (int64_t)gridDim.x * 4) {
+    const int64_t t = __builtin_amdgcn_readfirstlane(row_slot[r]) / K;
+    quant_row<T>(x + t * H, H, xq + r * H, sx + r, lane);
+  }
+}
+
+namespace {
+bool al16q(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+unsigned q_blocks(int64_t rows) { return (unsigned)std::min<int64_t>(4096, std::max<int64_t>(1, (rows + 3) / 4)); }
+}  // namespace
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst,
+                                  float* scale, void* stream) {
+  if (rows < 0 || cols < 16 || cols % 16 || ld < cols || ld % 8 || cols > INT32_MAX / 2 ||
+      (src_dtype != MOE_BF16 && src_dtype != MOE_F32))
+    return fail_arg("moe_quant_rows_fp8: bad arguments rows=%lld cols=%lld ld=%lld (need cols %% 16 == 0, ld >= cols, "
+                    "ld %% 8 == 0, bf16 or fp32)", (long long)rows, (long long)cols, (long long)ld);
+  if (rows == 0) return 0;
+  if (!src || !dst || !scale || !al16q(src) || !al16q(dst)) return fail_arg("moe_quant_rows_fp8: null or misaligned pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (src_dtype == MOE_BF16 && cols <= 32 * 512) {
+    // one pass: the row in registers (8 to 32 words a lane)
+    const auto* sp = static_cast<const uint16_t*>(src);
+    auto* dp = static_cast<uint8_t*>(dst);
+    if (cols <= 8 * 512)
+      MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8_reg<8>, dim3(q_blocks(rows)), dim3(256), 0, s, sp, rows,
+                 (int)cols, ld, dp, scale);
+    else if (cols <= 16 * 512)
+      MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8_reg<16>, dim3(q_blocks(rows)), dim3(256), 0, s, sp, rows,
+                 (int)cols, ld, dp, scale);
+    else
+      MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8_reg<32>, dim3(q_blocks(rows)), dim3(256), 0, s, sp, rows,
+                 (int)cols, ld, dp, scale);
+  } else if (src_dtype == MOE_BF16)
+    MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8<uint16_t>, dim3(q_blocks(rows)), dim3(256), 0, s,
+               static_cast<const uint16_t*>(src), rows, (int)cols, ld, static_cast<uint8_t*>(dst), scale);
+  else
+    MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8<float>, dim3(q_blocks(rows)), dim3(256), 0, s,
+               static_cast<const float*>(src), rows, (int)cols, ld, static_cast<uint8_t*>(dst), scale);
+  return check_launch("moe_quant_rows_fp8");
+}
+
+extern "C" int moe_permute_fp8(const void* x, int x_dtype, const int32_t* row_slot, const int32_t* offsets, int64_t E,
+                               int64_t K, int64_t H, int64_t R, void* xq, float* sx, void* stream) {
+  if (E < 1 || K < 1 || R < 0 || H < 16 || H % 16 || H > INT32_MAX / 2 || (x_dtype != MOE_BF16 && x_dtype != MOE_F32))
+    return fail_arg("moe_permute_fp8: bad arguments (need H %% 16 == 0, bf16 or fp32 x)");
+  if (R == 0) return 0;
+  if (!x || !row_slot || !offsets || !xq || !sx || !al16q(x) || !al16q(xq))
+    return fail_arg("moe_permute_fp8: null or misaligned pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (x_dtype == MOE_BF16)
+    MOE_LAUNCH("k_permute_fp8", k_permute_fp8<uint16_t>, dim3(q_blocks(R)), dim3(256), 0, s,
+               static_cast<const uint16_t*>(x), row_slot, offsets, (int)E, (int)K, (int)H, R,
+               static_cast<uint8_t*>(xq), sx);
+  else
+    MOE_LAUNCH("k_permute_fp8", k_permute_fp8<float>, dim3(q_blocks(R)), dim3(256), 0, s, static_cast<const float*>(x),
+               row_slot, offsets, (int)E, (int)K, (int)H, R, static_cast<uint8_t*>(xq), sx);
+  return check_launch("moe_permute_fp8");
+}

@@ -32,6 +32,13 @@
 //          act = silu(g) * u and the pre-activations hgu = [g | u]
 //   EPI 2  SwiGLU backward: C = dA; reads hgu and stores dh = [dg | du]
 //          with dg = dA u silu'(g), du = dA silu(g).
+//   operand mode 2 (both operands, "rows fp8"): e4m3 bytes, k contiguous, with fp32 scales per A row
+//          (sa) and per B row (sb, sb2 for the up rows of EPI1).  The host passes K and the leading
+//          dimensions in 16-bit units (two fp8 per unit), so the DMA and the LDS tile are byte-for-byte
+//          those of a bf16 rows tile: a 64-unit slice holds 128 fp8 k.  Each k step of 64 uses
+//          v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales) on 32-byte fragments made of two 16-byte
+//          reads (A and B use the same k-to-lane map, which is all the product needs), and the
+//          epilogue multiplies by sa[row] * sb[col] before rounding.
 //
 // products (R = rows, per expert e):
 //   fwd1  [act | hgu] = xp  . [Wg_e ; Wu_e]^T      A rows(xp), B rows(W),  G0, EPI1
@@ -64,6 +71,9 @@ struct GemmArgs {
   const int* offsets;  // [E+1] row segments
   const int* tile_off; // [E+1] m-tile prefix (row-grouped, computed with this kernel's BM)
   const int* korder;   // [E] expert order of the k-grouped tiles (heaviest first per XCD range)
+  const float* sa;     // mode 2: scale of each A row [rows]
+  const float* sb;     // mode 2: scale of each B row [E][N] (EPI1: gate rows [E][F])
+  const float* sb2;    // mode 2, EPI1: scale of the up rows [E][F]
   int E;
   int M, N, K;         // k-grouped: M, N fixed; row-grouped: N, K fixed
 };
@@ -76,6 +86,7 @@ constexpr int GWM = 128;
 constexpr int GOPB = GBM * GBK * 2;       // bytes of one operand tile per stage (32 KB): one ring unit
 constexpr int GCP = GBN + 8;              // epilogue C tile pitch (elements)
 constexpr int GSMEM = (GUNITS * GOPB > GBM * GCP * 2) ? GUNITS * GOPB : GBM * GCP * 2;
+constexpr int GSCALE = 2 * 256 * 4;       // mode 2: the tile's row and column scales, after the C tile
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
@@ -162,6 +173,19 @@ __device__ __forceinline__ i16x8 frag_cols(const uint8_t* t, int base, int ks, i
   return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+// fp8 operand of a 32x32x64 MFMA k step s of a rows tile: the 16-byte chunks 4s + h and 4s + 2 + h of row
+// base + l%32 (h = l/32), i.e. the bf16 fragments of quarters 2s and 2s+1.
+__device__ __forceinline__ i32x8 frag_rows_f8(const uint8_t* t, int base, int s, int lane) {
+  const u32x4 lo = __builtin_bit_cast(u32x4, frag_rows(t, base, 2 * s, lane));
+  const u32x4 hi = __builtin_bit_cast(u32x4, frag_rows(t, base, 2 * s + 1, lane));
+  return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+// e4m3 x e4m3 -> fp32 (block scales 127 = 1.0: the per-row / per-column scales are applied in the epilogue)
+__device__ __forceinline__ f32x16 mfma32x32x64_f8(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
 template <int AMODE, int BMODE, int GROUP, int EPI, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   constexpr int GNT = NW * 64;
@@ -170,7 +194,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   constexpr int GDMA = 2 * QPW;            // ... for both operands
   constexpr int NW_N = GBN / GWN;
   constexpr int MI = GWM / 32, NI = GWN / 32;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[GSMEM];
+  constexpr bool F8 = AMODE == 2;
+  static_assert((AMODE == 2) == (BMODE == 2), "fp8 mode applies to both operands");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GSMEM + (F8 ? GSCALE : 0)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -250,7 +276,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
 #pragma unroll
   for (int q = 0; q < QPW; ++q) {
     const int j = QPW * wv + q;
-    if constexpr (AMODE == 0) {
+    if constexpr (AMODE != 1) {
       const int i = 8 * j + (lane >> 3);
       a_kl[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
       a_src[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase + a_kl[q];
@@ -260,7 +286,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       a_src[q] = g.A + (int64_t)(kbase + a_kl[q]) * g.lda + mbase + (i < mlen ? i : 0);
     }
     b_src2[q] = nullptr;
-    if constexpr (BMODE == 0) {
+    if constexpr (BMODE != 1) {
       const int i = 8 * j + (lane >> 3);
       b_kl[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
       const int ic = min(i, nlen - 1);
@@ -290,7 +316,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   auto issue_a = [&](int kt, uint8_t* unit) {
     const int k0 = kt * GBK;
     uint8_t* const sa = unit + QPW * wv * 1024;
-    const int64_t step = AMODE == 0 ? (int64_t)k0 : (int64_t)k0 * g.lda;
+    const int64_t step = AMODE != 1 ? (int64_t)k0 : (int64_t)k0 * g.lda;
     if (k0 + GBK <= klen) {
 #pragma unroll
       for (int q = 0; q < QPW; ++q) lds_dma16(a_src[q] + step, lds_addr(sa + q * 1024));
@@ -304,7 +330,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     const int k0 = kt * GBK;
     const bool kfull = k0 + GBK <= klen;
     uint8_t* const sb = unit + QPW * wv * 1024;
-    const int64_t bld = BMODE == 0 ? 1 : g.ldb;
+    const int64_t bld = BMODE != 1 ? 1 : g.ldb;
     bool split = false;
     if constexpr (BMODE == 1 && GROUP == 0) split = g.b_split > 0 && k0 + GBK > g.b_split;
     if (!split) {
@@ -351,10 +377,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   auto frags = [&](const uint8_t* as, const uint8_t* bs, int ks, i16x8 (&fa)[MI], i16x8 (&fb)[NI]) {
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
-      fa[mi] = AMODE == 0 ? frag_rows(as, wm0 + mi * 32, ks, lane) : frag_cols(as, wm0 + mi * 32, ks, lane);
+      fa[mi] = AMODE != 1 ? frag_rows(as, wm0 + mi * 32, ks, lane) : frag_cols(as, wm0 + mi * 32, ks, lane);
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
-      fb[ni] = BMODE == 0 ? frag_rows(bs, wn0 + ni * 32, ks, lane) : frag_cols(bs, wn0 + ni * 32, ks, lane);
+      fb[ni] = BMODE != 1 ? frag_rows(bs, wn0 + ni * 32, ks, lane) : frag_cols(bs, wn0 + ni * 32, ks, lane);
   };
   auto mma = [&](const i16x8 (&fa)[MI], const i16x8 (&fb)[NI]) {
 #pragma unroll
@@ -369,7 +395,44 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   // quarter of stage kt every wave waits for stage kt+1 (the only DMA group in flight) and for its
   // own reads of stage kt; one barrier makes both visible workgroup-wide, and stage kt's two units
   // are refilled with stage kt+2 while the last quarter's MFMAs run.
-  if (nk > 0) {
+  if constexpr (F8) {
+    // fp8: two 64-k steps per slice; each step's fragments are read and consumed in turn (the other wave
+    // of the SIMD covers the read latency), one barrier per slice as above
+    if (nk > 0) {
+      issue_unit(0);
+      issue_unit(1);
+      if (nk > 1) {
+        issue_unit(2);
+        issue_unit(3);
+      }
+      if (nk > 1) wait_vmcnt<2 * QPW>();
+      else wait_vmcnt<0>();
+      lds_barrier();
+      for (int kt = 0; kt < nk; ++kt) {
+        const uint8_t* const ca = unit_ptr(2 * kt);
+        const uint8_t* const cb = unit_ptr(2 * kt + 1);
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          i32x8 fa[MI], fb[NI];
+#pragma unroll
+          for (int mi = 0; mi < MI; ++mi) fa[mi] = frag_rows_f8(ca, wm0 + mi * 32, st, lane);
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(cb, wn0 + ni * 32, st, lane);
+#pragma unroll
+          for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32x32x64_f8(fa[mi], fb[ni], acc[mi][ni]);
+        }
+        wait_vmcnt_lgkm0<0>();  // stage kt+1 landed; this wave's reads of stage kt are done
+        lds_barrier();
+        if (kt + 2 < nk) {
+          issue_unit(2 * kt + 4);
+          issue_unit(2 * kt + 5);
+        }
+      }
+      wait_vmcnt<0>();
+    }
+  } else if (nk > 0) {
     issue_unit(0);
     issue_unit(1);
     if (nk > 1) {
@@ -417,15 +480,44 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   // acc[mi][ni][j] = C[wm0 + mi*32 + (j/4)*8 + (lane/32)*4 + j%4][wn0 + ni*32 + lane%32]
   constexpr int CP = GCP;
   uint16_t* cs = reinterpret_cast<uint16_t*>(smem);
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
-        cs[r * CP + wn0 + ni * 32 + (lane & 31)] = f2bf(acc[mi][ni][j]);
+  if constexpr (F8) {
+    // the tile's row scales [256] and column scales [256] (rows / columns past the tile clamped)
+    float* s_sc = reinterpret_cast<float*>(smem + GSMEM);
+    if (tid < 256) {
+      s_sc[tid] = g.sa[mbase + min(tid, mlen - 1)];
+      float sb;
+      if constexpr (EPI == 1) {
+        const int f = min(nt * (GBN / 2) + (tid >> 6) * 32 + (tid & 31), g.F - 1);
+        sb = (((tid >> 5) & 1) ? g.sb2 : g.sb)[(int64_t)e * g.F + f];
+      } else {
+        sb = g.sb[(int64_t)e * g.N + min(n0 + tid, g.N - 1)];
       }
+      s_sc[256 + tid] = sb;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        const int c = wn0 + ni * 32 + (lane & 31);
+        const float sc = s_sc[256 + c];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+          cs[r * CP + c] = f2bf(acc[mi][ni][j] * s_sc[r] * sc);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+          cs[r * CP + wn0 + ni * 32 + (lane & 31)] = f2bf(acc[mi][ni][j]);
+        }
+  }
   __syncthreads();
   const int BN = GBN, BM = GBM, NT = GNT;
   if constexpr (EPI == 1) {
@@ -616,6 +708,73 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   b.N = (int)H;
   b.K = (int)F;
   return launch<0, 0, 0, 0, kNW_fwd2>("k_gemm_swiglu_fwd2", s, b, R);
+}
+
+extern "C" size_t moe_swiglu_fwd_fp8_workspace(int64_t R, int64_t F, int64_t E) {
+  // tile prefix + expert order, then act in e4m3 [R, F] and its row scales [R]
+  return moe_swiglu_workspace(E) + (((size_t)R * F + 255) & ~(size_t)255) + (((size_t)R * 4 + 255) & ~(size_t)255);
+}
+
+extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* wg_q, const float* sg, const void* wu_q,
+                                  const float* su, const void* wd_q, const float* sd, const int32_t* offsets, int64_t R,
+                                  int64_t H, int64_t F, int64_t E, void* act, void* hgu, void* y, void* workspace,
+                                  size_t ws_bytes, void* stream) {
+  if (R < 0 || H < 16 || F < 32 || E < 1 || E > 1024 || H % 16 || F % 32)
+    return fail_arg("moe_swiglu_fwd_fp8: bad shape R=%lld H=%lld F=%lld E=%lld (need H%%16==0, F%%32==0)",
+                    (long long)R, (long long)H, (long long)F, (long long)E);
+  if (R == 0) return 0;
+  if (!xq || !sx || !wg_q || !sg || !wu_q || !su || !wd_q || !sd || !offsets || !act || !hgu || !y || !a16(xq) ||
+      !a16(wg_q) || !a16(wu_q) || !a16(wd_q) || !a16(act) || !a16(hgu) || !a16(y))
+    return fail_arg("moe_swiglu_fwd_fp8: null or misaligned pointer");
+  if (ws_bytes < moe_swiglu_fwd_fp8_workspace(R, F, E) || !workspace)
+    return set_error("moe_swiglu_fwd_fp8: workspace"), MOE_EWORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  int* tile_off = reinterpret_cast<int*>(ws);
+  int* korder = tile_off + (E + 1);
+  uint8_t* actq = reinterpret_cast<uint8_t*>(ws + moe_swiglu_workspace(E));
+  float* sact = reinterpret_cast<float*>(ws + moe_swiglu_workspace(E) + (((size_t)R * F + 255) & ~(size_t)255));
+  MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off, korder);
+  // fwd1: [act | hgu] = (xq sx) . ([Wg ; Wu] [sg ; su])^T; fp8 matrices are addressed in 16-bit units
+  GemmArgs a{};
+  a.offsets = offsets;
+  a.tile_off = tile_off;
+  a.E = (int)E;
+  a.F = (int)F;
+  a.A = static_cast<const uint16_t*>(xq);
+  a.lda = H / 2;
+  a.B = static_cast<const uint16_t*>(wg_q);
+  a.B2 = static_cast<const uint16_t*>(wu_q);
+  a.ldb = H / 2;
+  a.b_estride = F * H / 2;
+  a.sa = sx;
+  a.sb = sg;
+  a.sb2 = su;
+  a.C = static_cast<uint16_t*>(act);
+  a.C2 = static_cast<uint16_t*>(hgu);
+  a.ldc = F;
+  a.N = (int)(2 * F);
+  a.K = (int)(H / 2);
+  if (int rc = launch<2, 2, 0, 1, kNW_fwd1>("k_gemm_swiglu_fwd1_fp8", s, a, R)) return rc;
+  // act -> e4m3 with a scale per row, then fwd2: y = (actq sact) . (Wd sd)^T
+  if (int rc = moe_quant_rows_fp8(act, MOE_BF16, R, F, F, actq, sact, stream)) return rc;
+  GemmArgs b{};
+  b.offsets = offsets;
+  b.tile_off = tile_off;
+  b.E = (int)E;
+  b.F = (int)F;
+  b.A = reinterpret_cast<const uint16_t*>(actq);
+  b.lda = F / 2;
+  b.B = static_cast<const uint16_t*>(wd_q);
+  b.ldb = F / 2;
+  b.b_estride = H * F / 2;
+  b.sa = sact;
+  b.sb = sd;
+  b.C = static_cast<uint16_t*>(y);
+  b.ldc = H;
+  b.N = (int)H;
+  b.K = (int)(F / 2);
+  return launch<2, 2, 0, 0, kNW_fwd2>("k_gemm_swiglu_fwd2_fp8", s, b, R);
 }
 
 extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* hgu, const void* w_gate,

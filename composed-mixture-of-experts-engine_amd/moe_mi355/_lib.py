@@ -65,6 +65,12 @@ _SIGNATURES = {
         [_P, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _F32, _F32, _P, _I64, _I64, _I64, _I64,
          _P, _P, _P, _P, _SZ, _P],
     ),
+    "moe_quant_rows_fp8": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _P]),
+    "moe_permute_fp8": (_I32, [_P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "moe_swiglu_fwd_fp8_workspace": (_SZ, [_I64, _I64, _I64]),
+    "moe_swiglu_fwd_fp8": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]
+    ),
     "moe_telemetry_fields": (_I32, []),
     "moe_telemetry_record": (_I32, [_P, _I64, _I64, _I64, _F32, _P, _I64, _P, _P]),
     "moe_swiglu_workspace": (_SZ, [_I64]),

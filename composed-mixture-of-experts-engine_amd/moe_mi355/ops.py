@@ -426,6 +426,71 @@ def swiglu_forward(xp: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w
     return act, hgu, y
 
 
+# ---------------------------------------------------------------------------
+# fp8 (e4m3) forward of the expert FFN
+# ---------------------------------------------------------------------------
+def quant_rows_fp8(t: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Rows of ``t`` [..., cols] (bf16 / fp32) -> (e4m3 bytes uint8 [..., cols], fp32 scale [...]): scale =
+    absmax(row) / 448 (1 for a zero row), element = x * (448 / absmax) rounded to nearest even."""
+    dev = L.require_device(t)
+    t = t.contiguous()
+    cols = t.shape[-1]
+    rows = t.numel() // cols if cols else 0
+    q = torch.empty(t.shape, dtype=torch.uint8, device=dev)
+    sc = torch.empty(t.shape[:-1], dtype=torch.float32, device=dev)
+    if rows == 0:
+        return q, sc
+    rc = L.load().moe_quant_rows_fp8(t.data_ptr(), L.dtype_code(t.dtype), rows, cols, cols, q.data_ptr(),
+                                     sc.data_ptr(), L.stream_of(dev))
+    L.check(rc, "moe_quant_rows_fp8")
+    return q, sc
+
+
+def permute_fp8(x: torch.Tensor, p: Plan) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The quantized dispatch payload: (xq [N*K, H] uint8 e4m3, sx [N*K] f32); row r is x[row_slot[r] // K]
+    quantized (rows past offsets[E] are left unwritten)."""
+    dev = L.require_device(x)
+    x = x.contiguous()
+    H = x.shape[1]
+    xq = torch.empty((p.rows, H), dtype=torch.uint8, device=dev)
+    sx = torch.empty((p.rows,), dtype=torch.float32, device=dev)
+    if p.rows == 0:
+        return xq, sx
+    rc = L.load().moe_permute_fp8(x.data_ptr(), L.dtype_code(x.dtype), p.row_slot.data_ptr(), p.offsets.data_ptr(),
+                                  p.E, p.K, H, p.rows, xq.data_ptr(), sx.data_ptr(), L.stream_of(dev))
+    L.check(rc, "moe_permute_fp8")
+    return xq, sx
+
+
+def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16):
+    """fp8 forward of the SwiGLU experts: ``xq`` [R,H] uint8 e4m3 with row scales ``sx`` [R]; ``wq`` =
+    (gate [E,F,H], up [E,F,H], down [E,H,F]) e4m3 bytes with ``wscale`` = (sg [E,F], su [E,F], sd [E,H])
+    -> (act [R,F], hgu [R,2F], y [R,H]) bf16, as :func:`swiglu_forward`."""
+    wg, wu, wd = wq
+    sg, su, sd = wscale
+    dev = L.require_device(xq, sx, wg, wu, wd, sg, su, sd, offsets)
+    for t in (xq, wg, wu, wd):
+        if t.dtype != torch.uint8 or not t.is_contiguous():
+            raise TypeError("swiglu_forward_fp8: quantized operands are contiguous uint8 (e4m3 bytes)")
+    if out_dtype != torch.bfloat16:
+        raise TypeError("swiglu_forward_fp8: outputs are bfloat16")
+    R, H = xq.shape
+    E, F, _ = wg.shape
+    act = torch.empty((R, F), dtype=out_dtype, device=dev)
+    hgu = torch.empty((R, 2 * F), dtype=out_dtype, device=dev)
+    y = torch.empty((R, H), dtype=out_dtype, device=dev)
+    lib = L.load()
+    nbytes = lib.moe_swiglu_fwd_fp8_workspace(R, F, E)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_swiglu_fwd_fp8(
+        xq.data_ptr(), sx.contiguous().data_ptr(), wg.data_ptr(), sg.contiguous().data_ptr(), wu.data_ptr(),
+        su.contiguous().data_ptr(), wd.data_ptr(), sd.contiguous().data_ptr(), offsets.data_ptr(), R, H, F, E,
+        act.data_ptr(), hgu.data_ptr(), y.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+    )
+    L.check(rc, "moe_swiglu_fwd_fp8")
+    return act, hgu, y
+
+
 def swiglu_backward(dy, xp, act, hgu, w_gate, w_up, w_down, offsets):
     """-> (dxp [R,H], dw_gate [E,F,H], dw_up [E,F,H], dw_down [E,H,F])."""
     dev = L.require_device(dy, xp, act, hgu, w_gate, w_up, w_down, offsets)

@@ -248,6 +248,44 @@ class DistributedMoELayer(nn.Module):
             )
         return out
 
+    # ------------------------------------------------------------------
+    # fp8 (e4m3) forward, new: an inference variant of the fused expert path
+    # ------------------------------------------------------------------
+    def quantize_fp8(self):
+        """e4m3 copies of the expert weights with one fp32 scale per weight row (per output channel), made
+        on the GPU; kept until the weights change (their in-place version counters are checked)."""
+        key = tuple((t.data_ptr(), t._version) for t in (self.w_gate, self.w_up, self.w_down))
+        cache = getattr(self, "_fp8_cache", None)
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                q = [ops.quant_rows_fp8(t.detach()) for t in (self.w_gate, self.w_up, self.w_down)]
+            self._fp8_cache = (key, tuple(t for t, _ in q), tuple(sc for _, sc in q))
+        return self._fp8_cache[1], self._fp8_cache[2]
+
+    @torch.no_grad()
+    def forward_fp8(self, tokens: torch.Tensor) -> torch.Tensor:
+        """The layer's forward with an e4m3 dispatch payload and e4m3 expert GEMMs (no autograd): router and
+        planner as in ``forward``, the permute writes each token row quantized (one fp32 scale per row),
+        the gate/up and down projections run on the fp8 MFMA with per-row x per-channel scales, the
+        SwiGLU activations are quantized per row between them, and the combine is the bf16 one.  Needs
+        the fused bf16 expert layout (``self._fused()``) and hidden_dim % 16 == 0."""
+        if not self._fused():
+            raise NotImplementedError("forward_fp8 needs the built-in SwiGLU experts in bfloat16")
+        shape = tokens.shape
+        flat = tokens.reshape(-1, shape[-1])
+        idx, weights, _cnt = self.router(flat)
+        N = flat.shape[0]
+        capacity = (
+            math.ceil(self.capacity_factor * N * self.top_k / self.num_experts) if self.capacity_dropping else -1
+        )
+        p = ops.plan(idx, self.num_experts, capacity=capacity, layout=_LAYOUTS[self.layout])
+        self.last_plan = p
+        wq, ws = self.quantize_fp8()
+        xq, sx = ops.permute_fp8(flat, p)
+        _act, _hgu, y = ops.swiglu_forward_fp8(xq, sx, wq, ws, p.offsets)
+        out = ops.combine(y, weights, p)
+        return out.reshape(shape)
+
     def _forward_per_expert(self, flat: torch.Tensor, weights: torch.Tensor, p: ops.Plan) -> torch.Tensor:
         """Dispatch/combine kernels around per-expert module calls (custom experts, non-bf16 dtypes)."""
         xp = PermuteFn.apply(flat, p)

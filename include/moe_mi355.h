@@ -200,6 +200,36 @@ int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* 
                    void* workspace, size_t ws_bytes, void* stream);
 
 /* ----------------------------------------------------------------------
+ * fp8 (e4m3, OCP) forward of the expert FFN: a variant of moe_permute +
+ * moe_swiglu_fwd (moe_layer.py L:317-319 and the expert loop L:166-198,
+ * L:326-337) with half the dispatch bytes and the gfx950 fp8 MFMA.  Every
+ * quantized row carries one fp32 scale = absmax(row) / 448 (1 for a zero
+ * row); elements are x * (448 / absmax) in fp32 (1 for a zero row) rounded
+ * to nearest even.  The reference has
+ * no fp8 path: its results are the bf16 path's up to this quantization.
+ *
+ * moe_quant_rows_fp8: src [rows, ld] (MOE_BF16 / MOE_F32, first `cols`
+ * columns) -> dst [rows, cols] e4m3 bytes, scale [rows] f32.  cols % 16 == 0.
+ * moe_permute_fp8: the quantized dispatch payload: row r of xq [R, H] is
+ * token row_slot[r] / K of x quantized, sx [R] its scale (rows the plan
+ * leaves empty are not written).
+ * moe_swiglu_fwd_fp8: act, hgu, y as moe_swiglu_fwd (bf16) from xq / sx and
+ * the quantized weights wg_q, wu_q [E, F, H], wd_q [E, H, F] with scales
+ * sg, su [E, F], sd [E, H] (moe_quant_rows_fp8 over the weight rows); act
+ * is quantized per row in the workspace before the down projection.
+ * H % 16 == 0, F % 32 == 0.
+ * ---------------------------------------------------------------------- */
+int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst,
+                       float* scale, void* stream);
+int moe_permute_fp8(const void* x, int x_dtype, const int32_t* row_slot, const int32_t* offsets, int64_t E,
+                    int64_t K, int64_t H, int64_t R, void* xq, float* sx, void* stream);
+size_t moe_swiglu_fwd_fp8_workspace(int64_t R, int64_t F, int64_t E);
+int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* wg_q, const float* sg, const void* wu_q,
+                       const float* su, const void* wd_q, const float* sd, const int32_t* offsets, int64_t R,
+                       int64_t H, int64_t F, int64_t E, void* act, void* hgu, void* y, void* workspace,
+                       size_t ws_bytes, void* stream);
+
+/* ----------------------------------------------------------------------
  * RMSNorm in front of the router (the caller step before the routed path):
  * replaces RMSNorm.forward (moe-engine/pkg/models/moe.py L:83-86) as used by
  * ToyMoEBlock.forward (L:125-126, x + moe(norm(x))):

@@ -10,6 +10,9 @@ algorithm of the reference moe-engine hot path:
   the reference "positional" layout and the routed layout.
 * ``oracle.layer``   -- the SwiGLU expert and the full MoE layer forward /
   backward in both layouts.
+* ``oracle.norm``    -- the RMSNorm in front of the router and its backward.
+* ``oracle.fp8``     -- the e4m3 row quantization and the fp8 expert forward
+  (this build's own variant: the reference has no fp8 path).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
 leg may import this package, and only as the checker (or the timed CPU

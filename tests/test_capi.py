@@ -19,7 +19,8 @@ HEADER = os.path.join(REPO, "include", "moe_mi355.h")
 
 
 def _declared_functions():
-    src = open(HEADER).read()
+    with open(HEADER) as f:
+        src = f.read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     names = re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(moe_\w+)\s*\(", src, flags=re.M)
     return sorted(set(names))

@@ -1,0 +1,112 @@
+"""fp8 (e4m3) forward of the expert FFN on the GPU against oracle/fp8.py: row quantization and the quantized
+dispatch payload bit-exact, the fp8 grouped GEMMs within the bf16 output tolerance of the float64 product of
+the same quantized operands, and the layer's fp8 forward against both the oracle chain and the bf16 layer."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_util import TOL, assert_rel, dev, say
+
+from moe_mi355 import ops
+from oracle import fp8 as O8
+from pkg.distributed import build_topology
+from pkg.distributed.moe_layer import DistributedMoELayer
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(64, 16, torch.bfloat16), (300, 4096, torch.bfloat16),
+                                             (33, 14336, torch.bfloat16), (100, 512, torch.float32)])
+def test_quant_rows_bit_exact(rows, cols, dtype):
+    say(f"[fp8 quant] {rows}x{cols} {dtype}")
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * torch.logspace(-4, 4, rows).unsqueeze(1)).to(dtype)
+    x[rows // 2] = 0.0
+    q, s = ops.quant_rows_fp8(x.to(dev()))
+    rq, rs = O8.quant_rows(x)
+    assert torch.equal(s.cpu(), rs), "row scales"
+    assert torch.equal(q.cpu(), rq), "e4m3 bytes"
+
+
+@pytest.mark.parametrize("layout,cap", [("reference", -1), ("routed", -1), ("routed", 40)])
+def test_permute_fp8_bit_exact(layout, cap):
+    say(f"[fp8 permute] {layout} cap={cap}")
+    N, H, E, K = 257, 512, 8, 2
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(N, H, generator=g).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(N)])
+    p = ops.plan(idx.to(dev()), E, capacity=cap, layout=ops.LAYOUT_ROUTED if layout == "routed" else ops.LAYOUT_REFERENCE)
+    xq, sx = ops.permute_fp8(x.to(dev()), p)
+    rows = int(p.offsets[-1].item())
+    src = p.row_slot[:rows].cpu().long() // K
+    rq, rs = O8.quant_rows(x[src])
+    assert torch.equal(xq[:rows].cpu(), rq) and torch.equal(sx[:rows].cpu(), rs)
+
+
+def _weights(E, F, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    wg = (torch.randn(E, F, H, generator=g) * H ** -0.5).to(torch.bfloat16)
+    wu = (torch.randn(E, F, H, generator=g) * H ** -0.5).to(torch.bfloat16)
+    wd = (torch.randn(E, H, F, generator=g) * F ** -0.5).to(torch.bfloat16)
+    return wg, wu, wd
+
+
+@pytest.mark.parametrize("R,H,F,E,counts", [
+    (600, 256, 512, 4, [250, 0, 300, 50]),        # an empty expert, ragged segments, rows past offsets[E]
+    (512, 4096, 14336, 2, [300, 212]),            # the C4 expert shape
+    (96, 128, 64, 3, [1, 90, 5]),                 # segments shorter than a tile, F < a 256-column tile
+])
+def test_swiglu_forward_fp8_parity(R, H, F, E, counts):
+    say(f"[fp8 swiglu] R={R} H={H} F={F} E={E}")
+    g = torch.Generator().manual_seed(R + F)
+    xp = torch.randn(R, H, generator=g).to(torch.bfloat16)
+    wts = _weights(E, F, H, R + 1)
+    offsets = torch.tensor([0] + list(torch.tensor(counts).cumsum(0)), dtype=torch.int32)
+    d = dev()
+    xq, sx = ops.quant_rows_fp8(xp.to(d))
+    wq = [ops.quant_rows_fp8(w.to(d)) for w in wts]
+    act, hgu, y = ops.swiglu_forward_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets.to(d))
+    torch.cuda.synchronize()
+    used = int(offsets[-1])
+    oq = [O8.quant_rows(w) for w in wts]
+    for (q, s), (rq, rs) in zip(wq, oq):
+        assert torch.equal(q.cpu(), rq) and torch.equal(s.cpu(), rs)
+    rh, ra, ry = O8.swiglu_fwd_fp8(xq.cpu(), sx.cpu(), [q for q, _ in oq], [s for _, s in oq], offsets.tolist(),
+                                   act_in=act.cpu().float())
+    tol = TOL[torch.bfloat16]
+    assert_rel(hgu[:used], rh[:used], tol, "hgu")
+    # act from the kernel's own g, u (its hardware sigmoid), then y from the kernel's act quantized
+    g_, u_ = hgu[:used, :F].double().cpu(), hgu[:used, F:].double().cpu()
+    assert_rel(act[:used], torch.nn.functional.silu(g_) * u_, tol, "act")
+    assert_rel(y[:used], ry[:used], tol, "y")
+
+
+def test_layer_forward_fp8():
+    say("[fp8 layer]")
+    torch.manual_seed(3)
+    N, H, F, E, K = 384, 512, 1024, 8, 2
+    layer = DistributedMoELayer(H, F, E, K, build_topology(), dtype=torch.bfloat16).to(dev())
+    x = torch.randn(N, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(dev())
+    with torch.no_grad():
+        ref = layer(x)
+    out = layer.forward_fp8(x)
+    assert out.shape == ref.shape and out.dtype == ref.dtype
+    # the fp8 forward follows the bf16 one up to the e4m3 rounding of x, the weights and act
+    err = ((out.float() - ref.float()).abs().max() / ref.float().abs().max()).item()
+    assert err < 0.1, err
+    # and it is the oracle chain exactly (within the bf16 output tolerance) on the same plan
+    p = layer.last_plan
+    wq, ws = layer.quantize_fp8()
+    xq, sx = ops.permute_fp8(x, p)
+    act, _hgu, y = ops.swiglu_forward_fp8(xq, sx, wq, ws, p.offsets)
+    out2 = ops.combine(y, layer.router(x)[1], p)
+    assert torch.equal(out2, out)
+    # weights changed in place -> the cached e4m3 copy is rebuilt
+    before = layer.quantize_fp8()[0][0].clone()
+    with torch.no_grad():
+        layer.w_gate.mul_(2.0)
+    after = layer.quantize_fp8()[0][0]
+    assert torch.equal(before, after)  # doubling every row leaves the e4m3 bytes as they were ...
+    assert torch.allclose(layer.quantize_fp8()[1][0], 2.0 * ops.quant_rows_fp8(layer.w_gate.detach() / 2.0)[1])

@@ -1,0 +1,76 @@
+"""The fp8 oracle (oracle/fp8.py) against closed forms, known e4m3 encodings and brute-force loops (the
+reference has no fp8 path, so nothing of the reference's pins it)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import fp8 as O8
+
+pytestmark = pytest.mark.cpu
+
+
+def test_known_encodings():
+    q, s = O8.quant_rows(torch.tensor([[1.0, 448.0, -448.0, 0.0]]))
+    assert s.item() == 1.0
+    assert q[0].tolist() == [0x38, 0x7E, 0xFE, 0x00]
+
+
+def test_absmax_maps_to_448_and_zero_rows():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 96, generator=g) * torch.logspace(-3, 3, 64).unsqueeze(1)
+    x[5] = 0.0
+    q, s = O8.quant_rows(x)
+    d = O8.dequant(q, s)
+    amax_pos = x.abs().argmax(-1)
+    for r in range(64):
+        if r == 5:
+            assert s[r].item() == 1.0 and int(q[r].sum()) == 0
+            continue
+        v = q[r, amax_pos[r]].view(torch.float8_e4m3fn).float().item()
+        assert abs(v) == 448.0
+        assert s[r].item() == pytest.approx(x[r].abs().max().item() / 448.0, rel=1e-7)
+    # e4m3: 3 mantissa bits -> relative rounding error <= 2^-4 in the normal range, absolute <= scale * 2^-10
+    # below it (subnormal spacing 2^-9)
+    bound = torch.maximum(x.double().abs() * 2.0 ** -4, s.double().unsqueeze(1) * 2.0 ** -10)
+    assert bool(((d - x.double()).abs() <= bound + 1e-30).all())
+
+
+def test_multiplier_is_the_correctly_rounded_quotient():
+    """x * inv with inv = fl32(448 / absmax) exactly (as the kernel's fp32 division is): re-derive each
+    element's e4m3 value from a float64 quotient rounded once to fp32."""
+    g = torch.Generator().manual_seed(2)
+    # bf16 inputs (8 significant bits) land on e4m3 rounding ties often enough to expose a 1-ulp multiplier
+    x = (torch.randn(300, 4096, generator=g) * torch.logspace(-4, 4, 300).unsqueeze(1)).to(torch.bfloat16).float()
+    q, _ = O8.quant_rows(x)
+    inv = (448.0 / x.double().abs().amax(-1)).float()  # float64 division, rounded once
+    want = (x * inv.unsqueeze(1)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert torch.equal(q, want)
+    # torch's scalar / tensor (reciprocal times the scalar) differs in the last bit for many rows
+    loose = (x * (448.0 / x.abs().amax(-1)).unsqueeze(1)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert not torch.equal(q, loose)
+
+
+def test_planted_mistake_is_caught():
+    """An e4m3 'fnuz'-style maximum of 240 instead of 448 leaves the absmax element at +-240."""
+    x = torch.tensor([[3.0, -7.0, 1.0]])
+    v = x / (x.abs().amax(-1, keepdim=True) / 240.0)
+    assert v.abs().max().item() != 448.0
+    q, _ = O8.quant_rows(x)
+    assert q[0, 1].item() == 0xFE
+
+
+def test_swiglu_fwd_fp8_matches_loops():
+    g = torch.Generator().manual_seed(1)
+    R, H, F, E = 7, 16, 32, 3
+    x = torch.randn(R, H, generator=g)
+    wg, wu = torch.randn(E, F, H, generator=g) * 0.3, torch.randn(E, F, H, generator=g) * 0.3
+    wd = torch.randn(E, H, F, generator=g) * 0.3
+    xq, sx = O8.quant_rows(x)
+    wq = [O8.quant_rows(w) for w in (wg, wu, wd)]
+    offsets = [0, 3, 3, 6]  # expert 1 empty, row 6 past offsets[E]
+    hgu, act, y = O8.swiglu_fwd_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets)
+    yl = O8.swiglu_fwd_fp8_loops(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets)
+    assert torch.allclose(y, yl, rtol=0, atol=0) or (y - yl).abs().max().item() <= 2 ** -8 * yl.abs().max().item()
+    assert y[6].abs().max().item() == 0.0 and hgu[6].abs().max().item() == 0.0
