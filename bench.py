@@ -343,7 +343,8 @@ def run_fp8_fwd(args, torch, inp):
         "fp8_speedup": round(ms_bf16 / ms_fp8, 3),
         "expert_TFLOP_per_step": fwd_flops / 1e12,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": k8[dom]["TFLOPs"], "peak": MFMA_FP8_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(k8[dom]["TFLOPs"] / MFMA_FP8_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(k8[dom]["TFLOPs"] / MFMA_FP8_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(dom, f"{cfg.name}:fp8"),
                      "flops_per_launch": fl8[dom], "avg_us": k8[dom]["avg_us"]},
         "kernels_bf16": k16, "kernels_fp8": k8,
     }
@@ -486,6 +487,21 @@ def run_dispatch(args, torch):
             "GBps": round(total / (ms * 1e-3) / 1e9, 1), "kernels": kernels}
 
 
+def add_mfma_ceiling(roof, extra, fp8):
+    """The dense MFMA rate this GPU sustains in a memory-free loop of the GEMM's instruction (and the shader
+    clock under that load), beside the published peak: ``roof["frac_of_ceiling"]`` is the kernel's share of it."""
+    from moe_mi355 import _lib
+
+    tf, mhz = _lib.prof_mfma_ceiling(100000, fp8=fp8)
+    roof["ceiling"] = round(tf, 1)
+    roof["frac_of_ceiling"] = round(roof["achieved"] / tf, 4)
+    extra["mfma_ceiling"] = {"instruction": "v_mfma_scale_f32_32x32x64_f8f6f4" if fp8 else "v_mfma_f32_32x32x16_bf16",
+                             "TFLOPs": round(tf, 1), "frac_of_peak": round(tf / (MFMA_FP8_PEAK_TFLOPS if fp8
+                                                                                   else MFMA_BF16_PEAK_TFLOPS), 4),
+                             "shader_MHz": round(mhz)}
+    log(f"[bench] MFMA ceiling ({'fp8' if fp8 else 'bf16'}): {tf:.0f} TFLOP/s at {mhz:.0f} MHz")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -528,6 +544,7 @@ def main():
             extra["router"]["cpu_baseline"] = cpu_baseline_router(torch)
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
+        add_mfma_ceiling(roof, extra, fp8=False)
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
         config["layout"] = args.layout
     elif args.workload == "router":
@@ -547,6 +564,7 @@ def main():
         cpu = None
         value, unit, ms = main_res["fp8_tokens_per_s"], "tokens/s", main_res["fp8_ms_per_step"]
         roof = main_res.pop("roofline")
+        add_mfma_ceiling(roof, extra, fp8=True)
         config = {"workload": main_res.pop("workload"), "tokens": main_res.pop("tokens")}
     elif args.workload == "dispatch":
         main_res = run_dispatch(args, torch)

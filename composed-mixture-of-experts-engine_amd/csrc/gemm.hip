@@ -868,3 +868,101 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
     return launch<1, 1, 1, 0, kNW_dw1>("k_gemm_swiglu_dw1", s, a, R);
   }
 }
+
+// ---------------------------------------------------------------------------
+// MFMA ceiling (bench only): every CU runs one block of 8 waves (two per SIMD), each wave four independent
+// accumulator chains of the GEMM's MFMA (bf16 v_mfma_f32_32x32x16_bf16, or the e4m3
+// v_mfma_scale_f32_32x32x64_f8f6f4) with no memory traffic.  Wave 0 of each block stamps the shader clock
+// counter (s_memtime) and the constant 100 MHz counter (s_memrealtime) around its loop, so the host gets
+// the dense MFMA rate the chip sustains and the shader clock it runs at under that load.
+// ---------------------------------------------------------------------------
+namespace moe {
+template <bool F8>
+__global__ __launch_bounds__(512) void k_mfma_ceiling(int iters, unsigned long long* __restrict__ stamps,
+                                                      float* __restrict__ sink) {
+  f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  i32x8 fa, fb;
+  bf16x8 ba, bb;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    fa[i] = 0x38383838 + (int)(threadIdx.x & 7);  // e4m3 bytes near 1.0
+    fb[i] = 0x30303030 + i;
+    ba[i] = (__bf16)(1e-3f * (float)(threadIdx.x + i));
+    bb[i] = (__bf16)(2e-3f * (float)i);
+  }
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (F8) {
+      c0 = mfma32x32x64_f8(fa, fb, c0);
+      c1 = mfma32x32x64_f8(fa, fb, c1);
+      c2 = mfma32x32x64_f8(fa, fb, c2);
+      c3 = mfma32x32x64_f8(fa, fb, c3);
+    } else {
+      c0 = mfma32x32x16(ba, bb, c0);
+      c1 = mfma32x32x16(ba, bb, c1);
+      c2 = mfma32x32x16(ba, bb, c2);
+      c3 = mfma32x32x16(ba, bb, c3);
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += c0[i] + c1[i] + c2[i] + c3[i];
+  if (s == -1.2345e-30f) sink[0] = s;  // keeps the chains live; never true for these operands
+  if (threadIdx.x == 0) {
+    stamps[blockIdx.x * 2 + 0] = t1 - t0;
+    stamps[blockIdx.x * 2 + 1] = r1 - r0;
+  }
+}
+}  // namespace moe
+
+extern "C" int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, double* clock_mhz) {
+  if (iters < 1 || iters > (1 << 24) || !tflops || !clock_mhz)
+    return fail_arg("moe_prof_mfma_ceiling: bad arguments (1 <= iters <= 2^24, non-null outputs)");
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return check_launch("moe_prof_mfma_ceiling");
+  const int blocks = prop.multiProcessorCount;
+  unsigned long long* d_st = nullptr;
+  float* d_sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  std::vector<unsigned long long> h((size_t)blocks * 2);
+  float ms = 0.f;
+  if (hipMalloc(&d_st, h.size() * sizeof(unsigned long long)) != hipSuccess || hipMalloc(&d_sink, 16) != hipSuccess ||
+      hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    rc = check_launch("moe_prof_mfma_ceiling");
+  } else {
+    auto run = [&](int n) {
+      if (fp8)
+        hipLaunchKernelGGL(k_mfma_ceiling<true>, dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
+      else
+        hipLaunchKernelGGL(k_mfma_ceiling<false>, dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
+    };
+    run((int)std::min<int64_t>(iters, 2000));  // warm the clocks
+    hipEventRecord(e0, nullptr);
+    run((int)iters);
+    hipEventRecord(e1, nullptr);
+    if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess ||
+        hipMemcpy(h.data(), d_st, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost) != hipSuccess)
+      rc = check_launch("moe_prof_mfma_ceiling");
+  }
+  if (rc == 0) {
+    double sc = 0.0, sr = 0.0;
+    for (int b = 0; b < blocks; ++b) {
+      sc += (double)h[2 * b];
+      sr += (double)h[2 * b + 1];
+    }
+    const double per_mfma = fp8 ? 2.0 * 32 * 32 * 64 : 2.0 * 32 * 32 * 16;
+    *tflops = per_mfma * 4.0 * (double)iters * 8.0 * blocks / (ms * 1e-3) / 1e12;
+    *clock_mhz = sr > 0.0 ? 100.0 * sc / sr : 0.0;
+  }
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  if (d_st) hipFree(d_st);
+  if (d_sink) hipFree(d_sink);
+  return rc;
+}

@@ -1109,7 +1109,7 @@ typedef short sh4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) sh4 lds_sh4;
 
 template <int NTE>
-__global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 4 : 1))) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ wg,
                                                             const float* __restrict__ logits,
                                                             const int64_t* __restrict__ idx,
@@ -1121,7 +1121,8 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
                                                             int nht, uint16_t* __restrict__ dx,
                                                             float* __restrict__ ws_dw, uint16_t* __restrict__ g_out,
                                                             int g_pitch) {
-  constexpr int GP = 32 + 8;         // token-major G row pitch (32 expert slots)
+  constexpr int GS = NTE * 16;       // expert slots of a token-major G row
+  constexpr int GP = GS + 8;         // its pitch: 16 rows of one 16-byte read hit distinct bank groups
   constexpr int GTP = kSTC + 8;      // expert-major G row pitch
   __shared__ __attribute__((aligned(16))) uint16_t gs[kSTC * GP];
   __shared__ __attribute__((aligned(16))) uint16_t gts[NTE * 16 * GTP];
@@ -1170,7 +1171,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
     }
     if (r < nst * 32) {
 #pragma unroll
-      for (int c8 = 0; c8 < 32; c8 += 8) {
+      for (int c8 = 0; c8 < GS; c8 += 8) {
         u32x4 w;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1241,7 +1242,9 @@ __global__ __launch_bounds__(256) void k_router_dxdw_stream(const uint16_t* __re
     // dx: D[m = t][n = h] = sum_e G[t][e] wg[h][e], written over the x tile
 #pragma unroll
     for (int mk = 0; mk < 2; ++mk) {
-      const i16x8 a = *reinterpret_cast<const i16x8*>(&gs[(lr0 + mk * 16 + n) * GP + g * 8]);
+      // k = 32 expert slots per MFMA: the slots past GS are zero
+      const i16x8 a = g * 8 < GS ? *reinterpret_cast<const i16x8*>(&gs[(lr0 + mk * 16 + n) * GP + g * 8])
+                                 : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int nc = 0; nc < 4; ++nc) {
         const f32x4 d = mfma16x16x32(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, wB[nc]),
@@ -1625,9 +1628,10 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
     p.tc_len = std::max(64, cdiv(cdiv(N, want), 64) * 64);
     p.nchunk = cdiv(N, p.tc_len);
   } else if (p.stream) {
-    // ~768 blocks (three per CU); chunks of a multiple of 64 tokens, at most kSTC
+    // one round of blocks: four per CU with up to 16 experts (39 KB of LDS, at most 128 registers), two
+    // with more (the second expert tile's registers); chunks of a multiple of 64 tokens, at most kSTC
     const int nht = (int)(H / 256);
-    const int want = std::max(1, 768 / nht);
+    const int want = std::max(1, (E <= 16 ? 1024 : 512) / nht);
     p.tc_len = std::min(kSTC, std::max(64, cdiv(cdiv(N, want), 64) * 64));
     p.nchunk = cdiv(N, p.tc_len);
   } else if (p.mfma) {

@@ -32,6 +32,7 @@ _SIGNATURES = {
     "moe_prof_enable": (_I32, [_I32]),
     "moe_prof_summary": (_I32, [ctypes.c_char_p, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "moe_prof_kernel_name": (_I32, [_I64, ctypes.c_char_p, _SZ]),
+    "moe_prof_mfma_ceiling": (_I32, [_I64, _I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "moe_router_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
     "moe_router_fwd_lds_bytes": (_I64, [_I64, _I64, _I64, _I32, _I32]),
     "moe_router_fwd": (
@@ -143,6 +144,14 @@ def prof_summary() -> dict:
         out[name] = (int(n.value), float(ms.value))
         i += 1
     return out
+
+
+def prof_mfma_ceiling(iters: int = 100000, fp8: bool = False) -> tuple:
+    """(TFLOP/s, shader MHz) of a memory-free MFMA loop on every CU of the current device."""
+    tf, mhz = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    check(load().moe_prof_mfma_ceiling(int(iters), 1 if fp8 else 0, ctypes.byref(tf), ctypes.byref(mhz)),
+          "moe_prof_mfma_ceiling")
+    return float(tf.value), float(mhz.value)
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -65,6 +65,14 @@ int moe_prof_enable(int on);
 int moe_prof_summary(const char* kernel, int64_t* launches, double* total_ms);
 int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
 
+/* MFMA ceiling of the current device (bench only; no counterpart in the
+ * reference): one block of 8 waves per CU runs `iters` x 4 independent chains
+ * of the grouped GEMM's MFMA (fp8 = 0: bf16 32x32x16; 1: e4m3 32x32x64) with no
+ * memory traffic, timed with hipEvents on the null stream.  Returns the dense
+ * rate in TFLOP/s and the shader clock under that load in MHz (s_memtime
+ * ticks per 100 MHz s_memrealtime tick).  Allocates and synchronizes. */
+int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, double* clock_mhz);
+
 /* ------------------------------------------------------------------------
  * Router forward: logits = x @ wg (+ bias), p = softmax(logits), top-k of p
  * (descending, exact ties -> lower expert index), w = v / max(sum v, 1e-30),
