@@ -539,8 +539,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       }
       const int64_t row = mbase + r;
       *reinterpret_cast<u32x4*>(g.C + row * g.ldc + f) = av;
-      *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + f) = gv;
-      *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + g.F + f) = uv;
+      if (g.C2 != nullptr) {  // the pre-activations, kept for the backward (none for inference)
+        *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + f) = gv;
+        *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + g.F + f) = uv;
+      }
     }
   } else {
     constexpr int UPR = BN / 8;
@@ -666,8 +668,8 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
     return fail_arg("moe_swiglu_fwd: bad shape R=%lld H=%lld F=%lld E=%lld (need H%%8==0, F%%32==0)", (long long)R,
                     (long long)H, (long long)F, (long long)E);
   if (R == 0) return 0;
-  if (!xp || !w_gate || !w_up || !w_down || !offsets || !act || !hgu || !y || !a16(xp) || !a16(w_gate) ||
-      !a16(w_up) || !a16(w_down) || !a16(act) || !a16(hgu) || !a16(y))
+  if (!xp || !w_gate || !w_up || !w_down || !offsets || !act || !y || !a16(xp) || !a16(w_gate) ||
+      !a16(w_up) || !a16(w_down) || !a16(act) || (hgu && !a16(hgu)) || !a16(y))
     return fail_arg("moe_swiglu_fwd: null or misaligned pointer");
   if (ws_bytes < moe_swiglu_workspace(E) || !workspace) return set_error("moe_swiglu_fwd: workspace"), MOE_EWORKSPACE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -723,8 +725,8 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
     return fail_arg("moe_swiglu_fwd_fp8: bad shape R=%lld H=%lld F=%lld E=%lld (need H%%16==0, F%%32==0)",
                     (long long)R, (long long)H, (long long)F, (long long)E);
   if (R == 0) return 0;
-  if (!xq || !sx || !wg_q || !sg || !wu_q || !su || !wd_q || !sd || !offsets || !act || !hgu || !y || !a16(xq) ||
-      !a16(wg_q) || !a16(wu_q) || !a16(wd_q) || !a16(act) || !a16(hgu) || !a16(y))
+  if (!xq || !sx || !wg_q || !sg || !wu_q || !su || !wd_q || !sd || !offsets || !act || !y || !a16(xq) ||
+      !a16(wg_q) || !a16(wu_q) || !a16(wd_q) || !a16(act) || (hgu && !a16(hgu)) || !a16(y))
     return fail_arg("moe_swiglu_fwd_fp8: null or misaligned pointer");
   if (ws_bytes < moe_swiglu_fwd_fp8_workspace(R, F, E) || !workspace)
     return set_error("moe_swiglu_fwd_fp8: workspace"), MOE_EWORKSPACE;

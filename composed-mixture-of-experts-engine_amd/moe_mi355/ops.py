@@ -403,8 +403,9 @@ def unpermute_sum(dxp: torch.Tensor, p: Plan, addend: Optional[torch.Tensor] = N
 # SwiGLU grouped GEMM (bf16)
 # ---------------------------------------------------------------------------
 def swiglu_forward(xp: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
-                   offsets: torch.Tensor):
-    """xp [R,H]; w_gate/w_up [E,F,H]; w_down [E,H,F] (bf16, contiguous) -> (act [R,F], hgu [R,2F], y [R,H])."""
+                   offsets: torch.Tensor, keep_preact: bool = True):
+    """xp [R,H]; w_gate/w_up [E,F,H]; w_down [E,H,F] (bf16, contiguous) -> (act [R,F], hgu [R,2F], y [R,H]).
+    ``keep_preact=False`` (no backward follows) skips storing the pre-activations: hgu is None."""
     dev = L.require_device(xp, w_gate, w_up, w_down, offsets)
     for t in (xp, w_gate, w_up, w_down):
         if t.dtype != torch.bfloat16:
@@ -414,13 +415,13 @@ def swiglu_forward(xp: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w
     R, H = xp.shape
     E, F, _ = w_gate.shape
     act = torch.empty((R, F), dtype=xp.dtype, device=dev)
-    hgu = torch.empty((R, 2 * F), dtype=xp.dtype, device=dev)
+    hgu = torch.empty((R, 2 * F), dtype=xp.dtype, device=dev) if keep_preact else None
     y = torch.empty((R, H), dtype=xp.dtype, device=dev)
     lib = L.load()
     nbytes = lib.moe_swiglu_workspace(E)
     ws = L.workspace(nbytes, dev)
     rc = lib.moe_swiglu_fwd(xp.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(),
-                            offsets.data_ptr(), R, H, F, E, act.data_ptr(), hgu.data_ptr(), y.data_ptr(),
+                            offsets.data_ptr(), R, H, F, E, act.data_ptr(), L.ptr(hgu), y.data_ptr(),
                             ws.data_ptr(), nbytes, L.stream_of(dev))
     L.check(rc, "moe_swiglu_fwd")
     return act, hgu, y
@@ -462,10 +463,10 @@ def permute_fp8(x: torch.Tensor, p: Plan) -> Tuple[torch.Tensor, torch.Tensor]:
     return xq, sx
 
 
-def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16):
+def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, keep_preact: bool = True):
     """fp8 forward of the SwiGLU experts: ``xq`` [R,H] uint8 e4m3 with row scales ``sx`` [R]; ``wq`` =
     (gate [E,F,H], up [E,F,H], down [E,H,F]) e4m3 bytes with ``wscale`` = (sg [E,F], su [E,F], sd [E,H])
-    -> (act [R,F], hgu [R,2F], y [R,H]) bf16, as :func:`swiglu_forward`."""
+    -> (act [R,F], hgu [R,2F], y [R,H]) bf16, as :func:`swiglu_forward` (hgu None with keep_preact=False)."""
     wg, wu, wd = wq
     sg, su, sd = wscale
     dev = L.require_device(xq, sx, wg, wu, wd, sg, su, sd, offsets)
@@ -477,7 +478,7 @@ def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16):
     R, H = xq.shape
     E, F, _ = wg.shape
     act = torch.empty((R, F), dtype=out_dtype, device=dev)
-    hgu = torch.empty((R, 2 * F), dtype=out_dtype, device=dev)
+    hgu = torch.empty((R, 2 * F), dtype=out_dtype, device=dev) if keep_preact else None
     y = torch.empty((R, H), dtype=out_dtype, device=dev)
     lib = L.load()
     nbytes = lib.moe_swiglu_fwd_fp8_workspace(R, F, E)
@@ -485,7 +486,7 @@ def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16):
     rc = lib.moe_swiglu_fwd_fp8(
         xq.data_ptr(), sx.contiguous().data_ptr(), wg.data_ptr(), sg.contiguous().data_ptr(), wu.data_ptr(),
         su.contiguous().data_ptr(), wd.data_ptr(), sd.contiguous().data_ptr(), offsets.data_ptr(), R, H, F, E,
-        act.data_ptr(), hgu.data_ptr(), y.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+        act.data_ptr(), L.ptr(hgu), y.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
     )
     L.check(rc, "moe_swiglu_fwd_fp8")
     return act, hgu, y

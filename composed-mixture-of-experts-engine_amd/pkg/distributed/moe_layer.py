@@ -238,7 +238,9 @@ class DistributedMoELayer(nn.Module):
         p = ops.plan(idx, self.num_experts, capacity=capacity, layout=_LAYOUTS[self.layout])
         self.last_plan = p
         if self._fused():
-            out = ExpertsFn.apply(flat, weights, self.w_gate, self.w_up, self.w_down, p)
+            train = torch.is_grad_enabled() and any(
+                t.requires_grad for t in (flat, weights, self.w_gate, self.w_up, self.w_down))
+            out = ExpertsFn.apply(flat, weights, self.w_gate, self.w_up, self.w_down, p, train)
         else:
             out = self._forward_per_expert(flat, weights, p)
         if self.check_numerics:
@@ -282,7 +284,7 @@ class DistributedMoELayer(nn.Module):
         self.last_plan = p
         wq, ws = self.quantize_fp8()
         xq, sx = ops.permute_fp8(flat, p)
-        _act, _hgu, y = ops.swiglu_forward_fp8(xq, sx, wq, ws, p.offsets)
+        _act, _hgu, y = ops.swiglu_forward_fp8(xq, sx, wq, ws, p.offsets, keep_preact=False)
         out = ops.combine(y, weights, p)
         return out.reshape(shape)
 

@@ -189,7 +189,9 @@ int moe_unpermute_sum(const void* dxp, const void* addend, int dtype, const int3
  * expert segment:  act = silu(xp Wg_e^T) * (xp Wu_e^T),  y = act Wd_e^T,
  * with w_gate / w_up [E, F, H] and w_down [E, H, F] (the reference's
  * nn.Linear [out, in] layout per expert).  hgu [R, 2F] keeps the two
- * pre-activations [g | u] for the backward.  Replaces the expert loop of
+ * pre-activations [g | u] for the backward; it may be NULL when no backward
+ * follows (inference: the forward then stores only act and y; also for
+ * moe_swiglu_fwd_fp8).  Replaces the expert loop of
  * pkg/distributed/moe_layer.py L:326-337 over _SwiGLUExpert.forward
  * (L:197-198; F.linear at tp=1, pkg/distributed/tensor_parallel.py
  * L:117-121, L:195-199).

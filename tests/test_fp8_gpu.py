@@ -110,3 +110,38 @@ def test_layer_forward_fp8():
     after = layer.quantize_fp8()[0][0]
     assert torch.equal(before, after)  # doubling every row leaves the e4m3 bytes as they were ...
     assert torch.allclose(layer.quantize_fp8()[1][0], 2.0 * ops.quant_rows_fp8(layer.w_gate.detach() / 2.0)[1])
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_forward_without_preactivations(fp8):
+    """keep_preact=False (inference) stores no hgu and leaves act and y bit-identical."""
+    say(f"[swiglu no-preact] fp8={fp8}")
+    R, H, F, E = 600, 256, 512, 4
+    g = torch.Generator().manual_seed(11)
+    xp = torch.randn(R, H, generator=g).to(torch.bfloat16)
+    wts = _weights(E, F, H, 12)
+    offsets = torch.tensor([0, 250, 250, 550, 600], dtype=torch.int32).to(dev())
+    if fp8:
+        xq, sx = ops.quant_rows_fp8(xp.to(dev()))
+        wq = [ops.quant_rows_fp8(w.to(dev())) for w in wts]
+        run = lambda keep: ops.swiglu_forward_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets,
+                                                  keep_preact=keep)
+    else:
+        xd, wd = xp.to(dev()), [w.to(dev()) for w in wts]
+        run = lambda keep: ops.swiglu_forward(xd, *wd, offsets, keep_preact=keep)
+    a1, h1, y1 = run(True)
+    a2, h2, y2 = run(False)
+    assert h1 is not None and h2 is None
+    assert torch.equal(a1, a2) and torch.equal(y1, y2)
+
+
+def test_layer_no_grad_matches_training_forward():
+    say("[layer no_grad forward]")
+    torch.manual_seed(5)
+    layer = DistributedMoELayer(256, 512, 8, 2, build_topology(), dtype=torch.bfloat16).to(dev())
+    x = torch.randn(300, 256, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(dev())
+    out = layer(x)
+    assert out.requires_grad
+    with torch.no_grad():
+        ref = layer(x)
+    assert torch.equal(out.detach(), ref)
