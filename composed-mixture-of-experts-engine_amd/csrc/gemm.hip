@@ -544,17 +544,33 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + g.F + f) = uv;
       }
     }
-  } else {
+  } else if constexpr (EPI == 2) {
+    // SwiGLU backward: the pre-activations of 8 chunks per thread are requested together (clamped to the
+    // tile's first row and column where a chunk lies outside the tile), so the HBM reads of the epilogue
+    // overlap instead of costing one round trip per chunk
     constexpr int UPR = BN / 8;
-    for (int u = tid; u < BM * UPR; u += NT) {
-      const int r = u / UPR, cc = (u % UPR) * 8;
-      const int c = n0 + cc;
-      if (r >= mlen || c >= g.N) continue;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc]);
-      if constexpr (EPI == 2) {
+    constexpr int PB = 8;
+    static_assert((BM * UPR) % (NT * PB) == 0, "epilogue batches");
+    for (int u0 = tid; u0 < BM * UPR; u0 += NT * PB) {
+      u32x4 gvs[PB], uvs[PB];
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        const int u = u0 + i * NT;
+        const int r = u / UPR, c = n0 + (u % UPR) * 8;
+        const bool ok = r < mlen && c < g.N;
+        const int64_t src = (int64_t)(mbase + (ok ? r : 0)) * 2 * g.F + (ok ? c : n0);
+        gvs[i] = *reinterpret_cast<const u32x4*>(g.X + src);
+        uvs[i] = *reinterpret_cast<const u32x4*>(g.X + src + g.F);
+      }
+#pragma unroll
+      for (int i = 0; i < PB; ++i) {
+        const int u = u0 + i * NT;
+        const int r = u / UPR, cc = (u % UPR) * 8;
+        const int c = n0 + cc;
+        if (r >= mlen || c >= g.N) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc]);
         const int64_t row = mbase + r;
-        const u32x4 gv = *reinterpret_cast<const u32x4*>(g.X + row * 2 * (int64_t)g.F + c);
-        const u32x4 uv = *reinterpret_cast<const u32x4*>(g.X + row * 2 * (int64_t)g.F + g.F + c);
+        const u32x4 gv = gvs[i], uv = uvs[i];
         u32x4 dg, du;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -574,7 +590,16 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         }
         *reinterpret_cast<u32x4*>(g.C + row * g.ldc + c) = dg;
         *reinterpret_cast<u32x4*>(g.C + row * g.ldc + g.F + c) = du;
-      } else if constexpr (GROUP == 0) {
+      }
+    }
+  } else {
+    constexpr int UPR = BN / 8;
+    for (int u = tid; u < BM * UPR; u += NT) {
+      const int r = u / UPR, cc = (u % UPR) * 8;
+      const int c = n0 + cc;
+      if (r >= mlen || c >= g.N) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc]);
+      if constexpr (GROUP == 0) {
         *reinterpret_cast<u32x4*>(g.C + (int64_t)(mbase + r) * g.ldc + c) = v;
       } else {
         const int m = mbase + r;
