@@ -18,7 +18,9 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("rows,cols,dtype", [(64, 16, torch.bfloat16), (300, 4096, torch.bfloat16),
-                                             (33, 14336, torch.bfloat16), (100, 512, torch.float32)])
+                                             (33, 14336, torch.bfloat16), (100, 512, torch.float32),
+                                             (9, 20480, torch.bfloat16),   # past the register path: two passes
+                                             (7, 16400, torch.float32)])
 def test_quant_rows_bit_exact(rows, cols, dtype):
     say(f"[fp8 quant] {rows}x{cols} {dtype}")
     g = torch.Generator().manual_seed(rows + cols)
@@ -30,12 +32,13 @@ def test_quant_rows_bit_exact(rows, cols, dtype):
     assert torch.equal(q.cpu(), rq), "e4m3 bytes"
 
 
-@pytest.mark.parametrize("layout,cap", [("reference", -1), ("routed", -1), ("routed", 40)])
-def test_permute_fp8_bit_exact(layout, cap):
-    say(f"[fp8 permute] {layout} cap={cap}")
+@pytest.mark.parametrize("layout,cap,dtype", [("reference", -1, torch.bfloat16), ("routed", -1, torch.bfloat16),
+                                              ("routed", 40, torch.bfloat16), ("reference", -1, torch.float32)])
+def test_permute_fp8_bit_exact(layout, cap, dtype):
+    say(f"[fp8 permute] {layout} cap={cap} {dtype}")
     N, H, E, K = 257, 512, 8, 2
     g = torch.Generator().manual_seed(7)
-    x = torch.randn(N, H, generator=g).to(torch.bfloat16)
+    x = torch.randn(N, H, generator=g).to(dtype)
     idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(N)])
     p = ops.plan(idx.to(dev()), E, capacity=cap, layout=ops.LAYOUT_ROUTED if layout == "routed" else ops.LAYOUT_REFERENCE)
     xq, sx = ops.permute_fp8(x.to(dev()), p)
