@@ -538,6 +538,10 @@ def main():
         log(f"[bench] router: {extra['router']['ms_per_step']:.4f} ms/step")
         extra["norm_router"] = run_norm_router(args, torch)
         log(f"[bench] norm_router: {extra['norm_router']['ms_per_step']:.4f} ms/step")
+        extra["fp8_fwd"] = run_fp8_fwd(args, torch, inp)
+        add_mfma_ceiling(extra["fp8_fwd"]["roofline"], extra["fp8_fwd"], fp8=True)
+        log(f"[bench] fp8 forward: {extra['fp8_fwd']['fp8_ms_per_step']:.3f} ms/step "
+            f"(bf16 forward {extra['fp8_fwd']['bf16_ms_per_step']:.3f})")
         cpu = None if args.no_cpu_baseline else cpu_baseline_layer(torch, configs.C4, args.layout, inp)
         del inp
         if not args.no_cpu_baseline:
