@@ -82,6 +82,10 @@ __device__ __forceinline__ void quant_row_reg(const uint16_t* __restrict__ src, 
       amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(w[j][m] << 16)), fabsf(__uint_as_float(w[j][m] & 0xffff0000u))));
   }
   amax = wave_max(amax);
+  // the packed words are pinned here: otherwise the compiler keeps the first pass's unpacked floats for the
+  // second pass (twice the registers of the row: one wave per SIMD at 32 words a lane)
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) __asm__ volatile("" : "+v"(w[j]));
   const float sc = amax > 0.f ? amax / kE4M3Max : 1.f;
   const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
   if (lane == 0) *scale = sc;
