@@ -169,6 +169,11 @@ void set_error(const char* fmt, ...);
 int fail_arg(const char* fmt, ...);
 int check_launch(const char* what);
 
+// ---- e4m3 row quantization shared by the fp8 entry points (csrc/fp8.hip); row_limit (a device count, or
+// null) bounds the rows quantized to min(rows, *row_limit) ----
+int quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst, float* scale,
+                   const int* row_limit, hipStream_t s);
+
 // ---- optional per-kernel timing (host side; off unless moe_prof_enable(1)) ----
 // Brackets one launch with two hipEvents recorded on the launch stream.
 struct ProfScope {

@@ -1,8 +1,10 @@
 // e4m3 (OCP fp8) payloads of the expert FFN forward.
 //
-// Each row gets one fp32 scale, absmax / 448 (448 is the largest e4m3 value; an all-zero row gets 1), and
-// its elements are multiplied by inv = 448 / absmax (one division per row; 1 for a zero row) in fp32 and
-// rounded to nearest even by v_cvt_pk_fp8_f32.
+// Each row gets one fp32 scale, absmax / 448 (448 is the largest e4m3 value), and its elements are
+// multiplied by inv = 448 / absmax (one division per row) in fp32 and rounded to nearest even by
+// v_cvt_pk_fp8_f32.  A row whose absmax is below 2^-118 -- all-zero rows, and rows so small that 448 / absmax
+// would overflow fp32 (it does below 448 / FLT_MAX ~ 1.3e-36), turning 0 * inv into NaN -- is treated as a
+// zero row: scale 1, inv 1 (its elements, all below 2^-118, round to +-0).
 //
 // k_permute_fp8     the dispatch payload: row r of the permuted buffer is the quantized row of token
 //                   row_slot[r] / K (the rows k_permute copies), written at one byte per element -- half
@@ -17,6 +19,13 @@
 namespace moe {
 
 constexpr float kE4M3Max = 448.f;
+constexpr float kQuantTiny = 0x1p-118f;  // smallest absmax quantized with its own scale: 448 / 2^-118 < FLT_MAX
+
+__device__ __forceinline__ void row_scale(float amax, float& sc, float& inv) {
+  const bool live = amax >= kQuantTiny;
+  sc = live ? amax / kE4M3Max : 1.f;
+  inv = live ? kE4M3Max / amax : 1.f;
+}
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
@@ -51,8 +60,8 @@ __device__ __forceinline__ void quant_row(const T* __restrict__ src, int cols, u
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   }
   amax = wave_max(amax);
-  const float sc = amax > 0.f ? amax / kE4M3Max : 1.f;
-  const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+  float sc, inv;
+  row_scale(amax, sc, inv);
   if (lane == 0) *scale = sc;
   for (int c = lane * 8; c < cols; c += 512) {
     float v[8];
@@ -86,8 +95,8 @@ __device__ __forceinline__ void quant_row_reg(const uint16_t* __restrict__ src, 
   // second pass (twice the registers of the row: one wave per SIMD at 32 words a lane)
 #pragma unroll
   for (int j = 0; j < NCH; ++j) __asm__ volatile("" : "+v"(w[j]));
-  const float sc = amax > 0.f ? amax / kE4M3Max : 1.f;
-  const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+  float sc, inv;
+  row_scale(amax, sc, inv);
   if (lane == 0) *scale = sc;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
@@ -109,19 +118,29 @@ __device__ __forceinline__ void quant_row_reg(const uint16_t* __restrict__ src, 
 
 __device__ __forceinline__ int q_wave() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// Rows quantized: the first `rows`, or the first min(rows, *row_limit) when row_limit is given (a device count,
+// e.g. the rows the expert segments cover, offsets[E]).
+__device__ __forceinline__ int64_t q_rows(int64_t rows, const int* __restrict__ row_limit) {
+  return row_limit ? min(rows, (int64_t)max(*row_limit, 0)) : rows;
+}
+
 template <int NCH>
 __global__ __launch_bounds__(256) void k_quant_rows_fp8_reg(const uint16_t* __restrict__ src, int64_t rows, int cols,
                                                            int64_t ld, uint8_t* __restrict__ dst,
-                                                           float* __restrict__ scale) {
+                                                           float* __restrict__ scale,
+                                                           const int* __restrict__ row_limit) {
   const int lane = threadIdx.x & 63;
+  rows = q_rows(rows, row_limit);
   for (int64_t r = (int64_t)blockIdx.x * 4 + q_wave(); r < rows; r += (int64_t)gridDim.x * 4)
     quant_row_reg<NCH>(src + r * ld, cols, dst + r * cols, scale + r, lane);
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_quant_rows_fp8(const T* __restrict__ src, int64_t rows, int cols, int64_t ld,
-                                                       uint8_t* __restrict__ dst, float* __restrict__ scale) {
+                                                       uint8_t* __restrict__ dst, float* __restrict__ scale,
+                                                       const int* __restrict__ row_limit) {
   const int lane = threadIdx.x & 63;
+  rows = q_rows(rows, row_limit);
   for (int64_t r = (int64_t)blockIdx.x * 4 + q_wave(); r < rows; r += (int64_t)gridDim.x * 4)
     quant_row<T>(src + r * ld, cols, dst + r * cols, scale + r, lane);
 }
@@ -142,39 +161,43 @@ namespace {
 bool al16q(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 unsigned q_blocks(int64_t rows) { return (unsigned)std::min<int64_t>(4096, std::max<int64_t>(1, (rows + 3) / 4)); }
 }  // namespace
-}  // namespace moe
 
-using namespace moe;
-
-extern "C" int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst,
-                                  float* scale, void* stream) {
+int quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst, float* scale,
+                   const int* row_limit, hipStream_t s) {
   if (rows < 0 || cols < 16 || cols % 16 || ld < cols || ld % 8 || cols > INT32_MAX / 2 ||
       (src_dtype != MOE_BF16 && src_dtype != MOE_F32))
     return fail_arg("moe_quant_rows_fp8: bad arguments rows=%lld cols=%lld ld=%lld (need cols %% 16 == 0, ld >= cols, "
                     "ld %% 8 == 0, bf16 or fp32)", (long long)rows, (long long)cols, (long long)ld);
   if (rows == 0) return 0;
   if (!src || !dst || !scale || !al16q(src) || !al16q(dst)) return fail_arg("moe_quant_rows_fp8: null or misaligned pointer");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (src_dtype == MOE_BF16 && cols <= 32 * 512) {
     // one pass: the row in registers (8 to 32 words a lane)
     const auto* sp = static_cast<const uint16_t*>(src);
     auto* dp = static_cast<uint8_t*>(dst);
     if (cols <= 8 * 512)
       MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8_reg<8>, dim3(q_blocks(rows)), dim3(256), 0, s, sp, rows,
-                 (int)cols, ld, dp, scale);
+                 (int)cols, ld, dp, scale, row_limit);
     else if (cols <= 16 * 512)
       MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8_reg<16>, dim3(q_blocks(rows)), dim3(256), 0, s, sp, rows,
-                 (int)cols, ld, dp, scale);
+                 (int)cols, ld, dp, scale, row_limit);
     else
       MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8_reg<32>, dim3(q_blocks(rows)), dim3(256), 0, s, sp, rows,
-                 (int)cols, ld, dp, scale);
+                 (int)cols, ld, dp, scale, row_limit);
   } else if (src_dtype == MOE_BF16)
     MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8<uint16_t>, dim3(q_blocks(rows)), dim3(256), 0, s,
-               static_cast<const uint16_t*>(src), rows, (int)cols, ld, static_cast<uint8_t*>(dst), scale);
+               static_cast<const uint16_t*>(src), rows, (int)cols, ld, static_cast<uint8_t*>(dst), scale, row_limit);
   else
     MOE_LAUNCH("k_quant_rows_fp8", k_quant_rows_fp8<float>, dim3(q_blocks(rows)), dim3(256), 0, s,
-               static_cast<const float*>(src), rows, (int)cols, ld, static_cast<uint8_t*>(dst), scale);
+               static_cast<const float*>(src), rows, (int)cols, ld, static_cast<uint8_t*>(dst), scale, row_limit);
   return check_launch("moe_quant_rows_fp8");
+}
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst,
+                                  float* scale, void* stream) {
+  return quant_rows_fp8(src, src_dtype, rows, cols, ld, dst, scale, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int moe_permute_fp8(const void* x, int x_dtype, const int32_t* row_slot, const int32_t* offsets, int64_t E,

@@ -784,7 +784,8 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
   a.K = (int)(H / 2);
   if (int rc = launch<2, 2, 0, 1, kNW_fwd1>("k_gemm_swiglu_fwd1_fp8", s, a, R)) return rc;
   // act -> e4m3 with a scale per row, then fwd2: y = (actq sact) . (Wd sd)^T
-  if (int rc = moe_quant_rows_fp8(act, MOE_BF16, R, F, F, actq, sact, stream)) return rc;
+  // (rows past offsets[E] are never read by the down projection and are not quantized)
+  if (int rc = quant_rows_fp8(act, MOE_BF16, R, F, F, actq, sact, offsets + E, s)) return rc;
   GemmArgs b{};
   b.offsets = offsets;
   b.tile_off = tile_off;

@@ -6,14 +6,16 @@
 // dropped_token_fraction; RouterProfile fields from moe_router.py L:594-612, L:690-745).  Here one
 // single-lane kernel turns the router's statistics vector (whose finalize already counts the experts
 // without tokens) and the planner's drop count into one fixed-layout record of a ring buffer in device
-// memory; the caller copies the ring to the host only when it logs.
+// memory.  The ring's write cursor lives in device memory after the records and the kernel advances it
+// with an atomic add, so a launch replayed from a HIP graph appends a new record each time; the caller
+// copies the ring (cursor included) to the host only when it logs.
 #include "common.h"
 
 namespace moe {
 
 // Record layout (floats).
 enum TelField {
-  kTelStep = 0,         // caller's step number
+  kTelStep = 0,         // step number, stored as an int32 (the caller's, or the record's ordinal)
   kTelImbalance = 1,    // max(cnt) / mean(cnt)
   kTelZ = 2,            // mean_t logsumexp^2 (router_z_loss)
   kTelCntMean = 3,      // tokens_per_expert_mean
@@ -30,18 +32,21 @@ enum TelField {
 
 __global__ __launch_bounds__(64) void k_telemetry_record(const float* __restrict__ stats, int E, int64_t N, int K,
                                                          float capacity_factor, const int* __restrict__ ndrop,
-                                                         float step, float* __restrict__ rec) {
+                                                         int64_t step, float* __restrict__ ring, int capacity) {
   if (threadIdx.x != 0) return;
+  int* cursor = reinterpret_cast<int*>(ring + (int64_t)capacity * kTelFields);
+  const int n = atomicAdd(cursor, 1);  // records appended before this one
+  float* rec = ring + (int64_t)(n % capacity) * kTelFields;
   const float dispatched = stats[5], dead = stats[7];
-  const float capacity = fmaxf(capacity_factor * (float)N * (float)K, 1.f);
-  rec[kTelStep] = step;
+  const float cap = fmaxf(capacity_factor * (float)N * (float)K, 1.f);
+  rec[kTelStep] = __int_as_float(step >= 0 ? (int)step : n);
   rec[kTelImbalance] = stats[2];
   rec[kTelZ] = stats[0];
   rec[kTelCntMean] = stats[3];
   rec[kTelCntStd] = stats[4];
   rec[kTelDead] = dead;
   rec[kTelActive] = (float)E - dead;
-  rec[kTelEfficiency] = dispatched / capacity;
+  rec[kTelEfficiency] = dispatched / cap;
   rec[kTelDropped] = (ndrop != nullptr && N > 0) ? (float)ndrop[0] / ((float)N * (float)K) : 0.f;
   rec[kTelAux] = stats[1];
   rec[kTelNonfinite] = stats[6];
@@ -57,13 +62,13 @@ using namespace moe;
 extern "C" int moe_telemetry_fields(void) { return kTelFields; }
 
 extern "C" int moe_telemetry_record(const float* stats, int64_t E, int64_t N, int64_t K, float capacity_factor,
-                                    const int32_t* ndrop, int64_t step, float* record, void* stream) {
-  if (E < 1 || N < 0 || K < 1 || step < 0)
-    return fail_arg("moe_telemetry_record: bad arguments E=%lld N=%lld K=%lld step=%lld", (long long)E, (long long)N,
-                    (long long)K, (long long)step);
-  if (!stats || !record) return fail_arg("moe_telemetry_record: null pointer argument");
+                                    const int32_t* ndrop, int64_t step, float* ring, int64_t capacity, void* stream) {
+  if (E < 1 || N < 0 || K < 1 || step > INT32_MAX || capacity < 1 || capacity > (1 << 24))
+    return fail_arg("moe_telemetry_record: bad arguments E=%lld N=%lld K=%lld step=%lld capacity=%lld",
+                    (long long)E, (long long)N, (long long)K, (long long)step, (long long)capacity);
+  if (!stats || !ring) return fail_arg("moe_telemetry_record: null pointer argument");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   MOE_LAUNCH("k_telemetry_record", k_telemetry_record, dim3(1), dim3(64), 0, s, stats, (int)E, N, (int)K,
-             capacity_factor, ndrop, (float)step, record);
+             capacity_factor, ndrop, step, ring, (int)capacity);
   return check_launch("moe_telemetry_record");
 }

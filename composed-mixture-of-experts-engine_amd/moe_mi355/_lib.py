@@ -73,7 +73,7 @@ _SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]
     ),
     "moe_telemetry_fields": (_I32, []),
-    "moe_telemetry_record": (_I32, [_P, _I64, _I64, _I64, _F32, _P, _I64, _P, _P]),
+    "moe_telemetry_record": (_I32, [_P, _I64, _I64, _I64, _F32, _P, _I64, _P, _I64, _P]),
     "moe_swiglu_workspace": (_SZ, [_I64]),
     "moe_swiglu_fwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "moe_swiglu_bwd": (

@@ -4,9 +4,10 @@ The reference's train step builds its routing telemetry on the host every step: 
 ``RouterProfile`` (eight ``.item()`` reads, moe-engine/pkg/kernels/moe_router.py L:690-745) and the dispatch
 counts (``(dc == 0).sum().item()`` ..., moe-engine/train.py L:360-399).  ``RoutingTelemetry`` keeps the same
 fields as fixed-layout records in a ring buffer in device memory: ``record`` appends one with one kernel launch
-(``moe_telemetry_record``) on the current stream, with no host synchronisation (it can be captured in a HIP
-graph), and ``flush`` copies the records written since the last flush to the host at once and returns them as
-dicts keyed like the reference's ``StepRecord.routing`` block (train.py L:382-392).
+(``moe_telemetry_record``) on the current stream, with no host synchronisation, and ``flush`` copies the ring
+to the host at once and returns the records appended since the last flush as dicts keyed like the
+reference's ``StepRecord.routing`` block (train.py L:382-392).  The ring's write cursor is a device counter
+that the kernel advances, so a ``record`` captured in a HIP graph appends a new record on every replay.
 
 With ``MoERouter(..., sync_profile=False)`` a training step then has no routing-related synchronisation at
 all; ``MoERouter(..., z_loss_coef=w)`` makes the z-loss a differentiable term (``router.last_z_loss``), which is
@@ -40,12 +41,16 @@ _INT_FIELDS = ("step", "dead_expert_count", "active_experts", "nonfinite_logits"
 
 
 def records_from_rows(rows: torch.Tensor) -> List[Dict[str, float]]:
-    """Host rows [n, >= len(FIELDS)] of the ring -> one dict per record (counts as ints)."""
+    """Host float32 rows [n, >= len(FIELDS)] of the ring -> one dict per record (counts as ints; the step is
+    stored as int32 bits)."""
+    rows = rows.contiguous()
+    steps = rows.view(torch.int32)[:, 0].tolist()
     out = []
-    for r in rows.tolist():
+    for r, st in zip(rows.tolist(), steps):
         d = {}
         for i, name in enumerate(FIELDS):
             d[name] = int(round(r[i])) if name in _INT_FIELDS else float(r[i])
+        d["step"] = int(st)
         out.append(d)
     return out
 
@@ -60,9 +65,10 @@ class RoutingTelemetry:
         L.require_device(torch.empty(0, device=dev))
         self.capacity = int(capacity)
         self.fields = int(L.load().moe_telemetry_fields())
-        self.ring = torch.zeros((self.capacity, self.fields), dtype=torch.float32, device=dev)
-        self.written = 0  # records written so far (host counter: no device read)
-        self.flushed = 0
+        # capacity records, then one row whose first word (int32) is the device write cursor
+        self._buf = torch.zeros((self.capacity + 1, self.fields), dtype=torch.float32, device=dev)
+        self.ring = self._buf[: self.capacity]
+        self.flushed = 0  # records appended before the last flush
 
     def record(self, router, step: Optional[int] = None, layer=None, capacity_factor: Optional[float] = None) -> None:
         """Append the routing record of ``router``'s last forward (a ``MoERouter``).  ``layer`` (a
@@ -79,24 +85,22 @@ class RoutingTelemetry:
             plan = getattr(layer, "last_plan", None)
             if getattr(layer, "capacity_dropping", False) and plan is not None:
                 ndrop = plan.ndrop
-        dev = L.require_device(stats, self.ring, ndrop)
-        step = self.written if step is None else int(step)
-        slot = self.written % self.capacity
+        dev = L.require_device(stats, self._buf, ndrop)
         rc = L.load().moe_telemetry_record(
-            stats.data_ptr(), int(router.num_experts), N, int(router.top_k), cf, L.ptr(ndrop), step,
-            self.ring[slot].data_ptr(), L.stream_of(dev),
+            stats.data_ptr(), int(router.num_experts), N, int(router.top_k), cf, L.ptr(ndrop),
+            -1 if step is None else int(step), self._buf.data_ptr(), self.capacity, L.stream_of(dev),
         )
         L.check(rc, "moe_telemetry_record")
-        self.written += 1
 
     def flush(self) -> List[Dict[str, float]]:
-        """Records written since the last flush (the newest ``capacity`` of them), oldest first: one
-        device-to-host copy."""
-        n = min(self.written - self.flushed, self.capacity)
+        """Records appended since the last flush (the newest ``capacity`` of them), oldest first: one
+        device-to-host copy of the ring and its cursor."""
+        host = self._buf.to("cpu")
+        written = int(host.view(torch.int32)[self.capacity, 0])
+        n = min(written - self.flushed, self.capacity)
+        self.flushed = written
         if n <= 0:
             return []
-        first = (self.written - n) % self.capacity
-        host = self.ring.to("cpu")
+        first = (written - n) % self.capacity
         idx = [(first + i) % self.capacity for i in range(n)]
-        self.flushed = self.written
         return records_from_rows(host[idx])

@@ -80,7 +80,8 @@ class MoERouterInterface(nn.Module):
             raise ValueError(f"Token hidden dim {H} ≠ router hidden_dim {self.hidden_dim}.")
         idx, weights, dispatch_counts = self._kernel_router(tokens)
         kr = self._kernel_router
-        head = kr.last_stats_host if kr.sync_profile else kr.last_stats[:8].to("cpu")
+        prof = kr.last_profile  # resolves the forward's statistics (one device-to-host copy)
+        head = kr.last_stats_host
         total = int(round(float(head[5])))
         expected = N * self.top_k
         if total != expected:
@@ -93,12 +94,12 @@ class MoERouterInterface(nn.Module):
             expert_indices=idx,
             combine_weights=weights,
             dispatch_counts=dispatch_counts,
-            load_imbalance=float(head[2]),
-            router_z_loss=float(head[0]),
-            used_triton=True,
-            kernel_ms=kr.last_profile.kernel_ms if kr.last_profile else 0.0,
-            tokens_per_expert_mean=float(head[3]),
-            tokens_per_expert_std=float(head[4]),
+            load_imbalance=prof.expert_load_imbalance,
+            router_z_loss=prof.router_z_loss,
+            used_triton=prof.used_triton,
+            kernel_ms=prof.kernel_ms,
+            tokens_per_expert_mean=prof.tokens_per_expert_mean,
+            tokens_per_expert_std=prof.tokens_per_expert_std,
         )
 
     def capacity_budget(self, num_tokens: int) -> int:

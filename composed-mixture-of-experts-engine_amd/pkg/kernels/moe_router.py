@@ -70,6 +70,48 @@ class RouterProfile:
     router_z_loss: float
 
 
+def router_fwd_bytes(tokens: torch.Tensor, gate_w: torch.Tensor, k: int, w_dtype: torch.dtype) -> int:
+    """Bytes the router forward moves to and from HBM, each tensor once: tokens and gate read; logits and
+    logsumexp (fp32), top-k indices (int64) and weights, dispatch counts (int64) and the statistics vector
+    written.  The rate the profile reports is this over the launch's duration (the reference's figure counts
+    the same tensors at its own widths, L:371-379)."""
+    N, H = tokens.shape
+    E = gate_w.shape[1]
+    wsz = torch.empty((), dtype=w_dtype).element_size()
+    return (N * H * tokens.element_size() + H * E * gate_w.element_size() + N * E * 4 + N * 4
+            + N * k * (8 + wsz) + E * 8 + (_lib.STATS_HEAD + E) * 4)
+
+
+def _gbps(nbytes: int, ms: float) -> float:
+    return nbytes / (ms * 1e-3) / 1e9 if ms > 0.0 else 0.0
+
+
+class _LaunchTiming:
+    """Two timing events recorded on the current stream around a launch sequence; the elapsed time is read
+    only when asked for (it then waits for the second event).  Not recorded under graph capture."""
+
+    __slots__ = ("a", "b")
+
+    def __init__(self, a, b):
+        self.a, self.b = a, b
+
+    @classmethod
+    def start(cls, like: torch.Tensor) -> Optional["_LaunchTiming"]:
+        if not like.is_cuda or torch.cuda.is_current_stream_capturing():
+            return None
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        return cls(a, b)
+
+    def stop(self) -> None:
+        self.b.record()
+
+    def elapsed_ms(self) -> float:
+        self.b.synchronize()
+        return max(float(self.a.elapsed_time(self.b)), 0.0)
+
+
 def _reference_route_fp64(tokens: torch.Tensor, gate_w: torch.Tensor, k: int):
     """The reference's float64 PyTorch router (L:257-271).  Not shipped with this build: every routing call
     runs the gfx950 kernels, and the float64 restatement used to check them is test infrastructure (oracle/).
@@ -100,16 +142,21 @@ class MoERouterFunction(torch.autograd.Function):
         assert 1 <= k <= E
         if force_reference:
             _no_reference_path()
+        timing = _LaunchTiming.start(tokens) if report is not None else None
         idx, w, logits, _lse, _cnt, _stats = ops.router_forward(tokens, gate_w, k)
+        if timing is not None:
+            timing.stop()
         ctx.save_for_backward(tokens, gate_w, logits, idx)
         ctx.k = k
         ctx.set_materialize_grads(False)
         ctx.mark_non_differentiable(idx)
         if report is not None:
+            # The kernels' duration is read back only for a caller that asks for the report (the reference
+            # synchronises on its timing event in every forward, L:342): one event pair on the launch stream.
             report["used_triton"] = True
-            report["kernel_ms"] = 0.0
             report["sram_bytes"] = _fwd_lds_bytes(tokens, gate_w)
-            report["achieved_bw"] = 0.0
+            report["kernel_ms"] = timing.elapsed_ms() if timing is not None else 0.0
+            report["achieved_bw"] = _gbps(router_fwd_bytes(tokens, gate_w, k, w.dtype), report["kernel_ms"])
         return idx, w
 
     @staticmethod
@@ -157,7 +204,13 @@ def _compute_router_z_loss(logits: torch.Tensor) -> float:
 
 
 class MoERouter(torch.nn.Module):
-    """Top-k router module; the gate ``gate_w`` [H, E] is a learnable parameter."""
+    """Top-k router module; the gate ``gate_w`` [H, E] is a learnable parameter.
+
+    ``last_profile`` is built from the forward's statistics vector and the duration of its kernels (two
+    timing events on the launch stream).  With ``sync_profile=True`` (the default) the forward reads both
+    back at once -- the one device-to-host copy that also feeds the reference's conservation and NaN checks;
+    with ``sync_profile=False`` the forward does not synchronise and ``last_profile`` is resolved when it is
+    first read."""
 
     def __init__(
         self,
@@ -182,7 +235,8 @@ class MoERouter(torch.nn.Module):
         self.aux_loss_coef = float(aux_loss_coef)
         self.z_loss_coef = float(z_loss_coef)
         self.sync_profile = sync_profile
-        self.last_profile: Optional[RouterProfile] = None
+        self._profile: Optional[RouterProfile] = None
+        self._pending = None  # what a not-yet-read profile is built from
         self._last_logits: Optional[torch.Tensor] = None
         self.last_aux_loss: Optional[torch.Tensor] = None
         self.last_z_loss: Optional[torch.Tensor] = None
@@ -192,6 +246,17 @@ class MoERouter(torch.nn.Module):
         # Fixed (non-learnable) additive logit bias [E] f32, e.g. a load-skew
         # harness; unlike ``bias`` it keeps w differentiable.  None = off.
         self.register_buffer("logit_bias", None)
+
+    @property
+    def last_profile(self) -> Optional[RouterProfile]:
+        if self._pending is not None:
+            self._resolve()
+        return self._profile
+
+    @last_profile.setter
+    def last_profile(self, value: Optional[RouterProfile]) -> None:
+        self._pending = None
+        self._profile = value
 
     def forward(self, tokens: torch.Tensor, force_reference: bool = False):
         """Returns ``(topk_idx [N,K] int64, topk_w [N,K] tokens.dtype, dispatch_cnt [E] int64)``."""
@@ -206,10 +271,13 @@ class MoERouter(torch.nn.Module):
         if force_reference:
             _no_reference_path()
 
+        timing = _LaunchTiming.start(flat)
         idx, w, aux, z, logits, cnt, stats = RouterCore.apply(
             flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, self._logit_bias()
         )
-        return self._finish(flat, idx, w, aux, z, logits, cnt, stats)
+        if timing is not None:
+            timing.stop()
+        return self._finish(flat, idx, w, aux, z, logits, cnt, stats, timing)
 
     def forward_with_norm(self, tokens: torch.Tensor, norm_weight: torch.Tensor, eps: float):
         """Route ``rmsnorm(tokens)`` with the norm fused into the router's read of ``tokens``
@@ -217,11 +285,14 @@ class MoERouter(torch.nn.Module):
         ``xn`` is the normalised input the routing used, for the expert path."""
         flat = tokens.reshape(-1, tokens.shape[-1])
         assert flat.shape[1] == self.hidden_dim
+        timing = _LaunchTiming.start(flat)
         xn, idx, w, aux, z, logits, cnt, stats = NormRouterCore.apply(
             flat, norm_weight, float(eps), self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef,
             self._logit_bias(),
         )
-        idx, w, cnt = self._finish(flat, idx, w, aux, z, logits, cnt, stats)
+        if timing is not None:
+            timing.stop()
+        idx, w, cnt = self._finish(flat, idx, w, aux, z, logits, cnt, stats, timing)
         return xn, idx, w, cnt
 
     def _logit_bias(self):
@@ -230,21 +301,37 @@ class MoERouter(torch.nn.Module):
             bias = self.logit_bias if bias is None else bias.detach().float() + self.logit_bias
         return bias
 
-    def _finish(self, flat, idx, w, aux, z, logits, cnt, stats):
+    def _finish(self, flat, idx, w, aux, z, logits, cnt, stats, timing):
         N = flat.shape[0]
+        z_plain = None
         if self.bias is not None:
             # Reference semantics (L:677-687): with a bias the combine weights are
-            # recomputed under no_grad, so no gradient flows through w.
+            # recomputed under no_grad, so no gradient flows through w; _last_logits
+            # and the reported z statistic are computed without the bias (L:727-733).
             w = w.detach()
+            logits = logits - self.bias.detach().float()
+            z_plain = torch.logsumexp(logits, dim=-1).square().mean().reshape(1) if N else logits.new_zeros(1)
         self._last_logits = logits
         self.last_aux_loss = aux
         self.last_z_loss = z
         self.last_stats = stats
         self.last_num_tokens = N
-
+        self._profile = None
+        self._pending = (N, _fwd_lds_bytes(flat, self.gate_w), router_fwd_bytes(flat, self.gate_w, self.top_k,
+                                                                                   w.dtype), stats, z_plain, timing)
         if self.sync_profile:
-            head = stats[:8].to("cpu")  # the single device->host copy of this forward
-            self.last_stats_host = head
+            self._resolve(check=True)
+        return idx, w, cnt
+
+    def _resolve(self, check: bool = False) -> None:
+        """Build ``last_profile`` from the pending forward: one device-to-host copy of the statistics (after
+        which the forward's kernels, and so the second timing event, have completed)."""
+        N, lds, nbytes, stats, z_plain, timing = self._pending
+        self._pending = None
+        head = stats[:8] if z_plain is None else torch.cat([stats[:8], z_plain])
+        head = head.to("cpu")
+        self.last_stats_host = head[:8]
+        if check:
             total = int(round(float(head[STAT_CNT_TOTAL])))
             expected_total = N * self.top_k
             assert total == expected_total, (
@@ -252,14 +339,14 @@ class MoERouter(torch.nn.Module):
                 f"expected={expected_total} (N={N}, K={self.top_k})"
             )
             assert float(head[STAT_NONFINITE]) == 0.0, "NaN in expert indices (non-finite gate logits)"
-            self.last_profile = RouterProfile(
-                sram_bytes_per_block=_fwd_lds_bytes(flat, self.gate_w),
-                achieved_bandwidth_gbps=0.0,
-                kernel_ms=0.0,
-                used_triton=True,
-                tokens_per_expert_mean=float(head[STAT_CNT_MEAN]),
-                tokens_per_expert_std=float(head[STAT_CNT_STD]),
-                expert_load_imbalance=float(head[STAT_IMBALANCE]),
-                router_z_loss=float(head[STAT_Z]),
-            )
-        return idx, w, cnt
+        kernel_ms = timing.elapsed_ms() if timing is not None else 0.0
+        self._profile = RouterProfile(
+            sram_bytes_per_block=lds,
+            achieved_bandwidth_gbps=_gbps(nbytes, kernel_ms),
+            kernel_ms=kernel_ms,
+            used_triton=True,
+            tokens_per_expert_mean=float(head[STAT_CNT_MEAN]),
+            tokens_per_expert_std=float(head[STAT_CNT_STD]),
+            expert_load_imbalance=float(head[STAT_IMBALANCE]),
+            router_z_loss=float(head[STAT_Z] if z_plain is None else head[8]),
+        )

@@ -296,21 +296,23 @@ int moe_rmsnorm_router_bwd(const void* x, int x_dtype, const void* gamma, int ga
  * reads the RouterProfile of moe_router.py L:594-612 / L:690-745 and the
  * dispatch counts with .item() synchronisations every step).
  *
- * moe_telemetry_record writes one record of moe_telemetry_fields() floats
- * (16) at `record` (e.g. one slot of a ring buffer) from the router's stats
- * vector (stats_out of moe_router_fwd / moe_rmsnorm_router_fwd, same stream)
- * and, optionally, the planner's drop count (ndrop of moe_plan; null = no
- * capacity drops):
- *   [0] step  [1] load imbalance  [2] z statistic  [3] tokens/expert mean
+ * moe_telemetry_record appends one record of moe_telemetry_fields() floats (16) to a ring buffer in device
+ * memory from the router's stats vector (stats_out of moe_router_fwd / moe_rmsnorm_router_fwd, same stream)
+ * and, optionally, the planner's drop count (ndrop of moe_plan; null = no capacity drops):
+ *   [0] step (int32 bits: `step`, or the record's ordinal when step < 0)
+ *   [1] load imbalance  [2] z statistic  [3] tokens/expert mean
  *   [4] tokens/expert std  [5] dead experts  [6] active experts
  *   [7] routing efficiency = dispatched / (capacity_factor * N * K)
  *   [8] dropped fraction = ndrop / (N * K)  [9] aux statistic
  *   [10] non-finite logits  [11] dispatched slots  [12..15] zero
- * No host synchronisation; the caller copies its records when it logs.
+ * ring: capacity * 16 floats of records followed by one int32 write cursor (the number of records appended
+ * so far; zero it once before the first record).  Record n goes to slot n % capacity; the kernel advances
+ * the cursor with an atomic add, so a launch captured in a HIP graph appends a new record on every replay.
+ * No host synchronisation; the caller copies the ring (cursor included) when it logs.
  * ---------------------------------------------------------------------- */
 int moe_telemetry_fields(void);
 int moe_telemetry_record(const float* stats, int64_t E, int64_t N, int64_t K, float capacity_factor,
-                         const int32_t* ndrop, int64_t step, float* record, void* stream);
+                         const int32_t* ndrop, int64_t step, float* ring, int64_t capacity, void* stream);
 
 #ifdef __cplusplus
 }

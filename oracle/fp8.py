@@ -3,9 +3,10 @@
 The reference has no fp8 path (moe-engine's experts run in the model dtype: pkg/distributed/moe_layer.py
 L:166-198, L:326-337); the fp8 variant is this build's own, and its contract is stated here:
 
-* ``quant_rows`` -- one fp32 scale per row, ``absmax / 448`` (448 = the largest finite e4m3 value; 1 for a
-  zero row), elements ``x * (448 / absmax)`` (fp32; one division per row) rounded to nearest even into OCP
-  e4m3 (``torch.float8_e4m3fn``).
+* ``quant_rows`` -- one fp32 scale per row, ``absmax / 448`` (448 = the largest finite e4m3 value),
+  elements ``x * (448 / absmax)`` (fp32; one division per row) rounded to nearest even into OCP e4m3
+  (``torch.float8_e4m3fn``).  A row with absmax below 2^-118 (a zero row, or one so small that 448 / absmax
+  would overflow fp32 and turn its zeros into NaN) is a zero row: scale 1, elements ``x`` rounded (to +-0).
 * ``swiglu_fwd_fp8`` -- the grouped SwiGLU forward on the dequantized operands in float64: per expert segment
   ``hgu = (xq sx) (Wq sw)^T``, ``g`` and ``u`` rounded to bf16, ``act = silu(g) u`` rounded to bf16, ``act``
   quantized per row, ``y = (actq sa) (Wdq sd)^T`` rounded to bf16.
@@ -24,13 +25,14 @@ from typing import Sequence, Tuple
 import torch
 
 E4M3_MAX = 448.0
+QUANT_TINY = 2.0 ** -118  # smallest absmax quantized with its own scale (448 / 2^-118 < FLT_MAX)
 
 
 def quant_rows(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     """x [..., cols] -> (e4m3 bytes uint8 [..., cols], fp32 scale [...])."""
     v = x.float()
     amax = v.abs().amax(-1)
-    pos = amax > 0
+    pos = amax >= QUANT_TINY
     scale = torch.where(pos, amax / E4M3_MAX, torch.ones_like(amax))
     # a true tensor division (correctly rounded); torch's ``scalar / tensor`` is reciprocal-times-scalar
     inv = torch.where(pos, torch.full_like(amax, E4M3_MAX) / torch.where(pos, amax, torch.ones_like(amax)),

@@ -88,6 +88,32 @@ def test_function_report_and_five_gradients():
     assert torch.isfinite(x.grad).all() and torch.isfinite(gw.grad).all()
 
 
+def test_profile_times_the_router_kernels():
+    """kernel_ms comes from timing events around the router's launches and achieved_bandwidth_gbps is the
+    forward's byte count over that time (the reference's L:313-343, L:371-379), with and without the
+    forward's own synchronisation (sync_profile=False resolves the profile when it is read)."""
+    from pkg.kernels.moe_router import router_fwd_bytes
+
+    N, H, E, K = 4096, 1024, 16, 2
+    x = _tokens(N, H, seed=9, dtype=torch.bfloat16)
+    for sync in (True, False):
+        say(f"[profile timing] sync_profile={sync}")
+        router = MoERouter(hidden_dim=H, num_experts=E, top_k=K, dtype=torch.bfloat16, sync_profile=sync).to(dev())
+        router(x)
+        _, w, _ = router(x)
+        p = router.last_profile
+        assert 0.0 < p.kernel_ms < 1000.0
+        nbytes = router_fwd_bytes(x, router.gate_w, K, w.dtype)
+        assert abs(p.achieved_bandwidth_gbps - nbytes / (p.kernel_ms * 1e-3) / 1e9) <= 1e-6 * p.achieved_bandwidth_gbps
+        assert router.last_profile is p  # resolved once
+    report = {}
+    gw = router.gate_w.detach()
+    MoERouterFunction.apply(x, gw, K, False, report)
+    assert report["kernel_ms"] > 0.0
+    assert abs(report["achieved_bw"] - router_fwd_bytes(x, gw, K, x.dtype) / (report["kernel_ms"] * 1e-3) / 1e9) \
+        <= 1e-6 * report["achieved_bw"]
+
+
 def test_force_reference_is_not_shipped():
     x = _tokens(8, 16, seed=7)
     gw = torch.zeros(16, 4, device=dev())

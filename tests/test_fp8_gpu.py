@@ -32,6 +32,28 @@ def test_quant_rows_bit_exact(rows, cols, dtype):
     assert torch.equal(q.cpu(), rq), "e4m3 bytes"
 
 
+@pytest.mark.parametrize("cols,dtype", [(4096, torch.bfloat16), (20480, torch.bfloat16), (512, torch.float32)])
+def test_quant_tiny_rows_are_zero_rows(cols, dtype):
+    """Rows with absmax below 2^-118 (down to bf16 / fp32 subnormals) quantize as zero rows -- scale 1, bytes
+    +-0, never NaN -- bit-exactly as the oracle; a row at exactly 2^-118 keeps its own scale."""
+    say(f"[fp8 quant tiny rows] cols={cols} {dtype}")
+    g = torch.Generator().manual_seed(cols)
+    x = torch.randn(6, cols, generator=g)
+    x[0] *= 1e-37
+    x[1] *= 1e-39                      # subnormal in fp32 and bf16
+    x[2] = 0.0
+    x[2, 3] = 2.0 ** -118
+    x[3] *= 2.0 ** -120
+    x[4] = -3e-37
+    x = x.to(dtype)
+    q, s = ops.quant_rows_fp8(x.to(dev()))
+    rq, rs = O8.quant_rows(x)
+    assert torch.equal(s.cpu(), rs), "row scales"
+    assert torch.equal(q.cpu(), rq), "e4m3 bytes"
+    assert not bool(torch.isnan(O8.dequant(q.cpu(), s.cpu())).any())
+    assert float(s[2]) != 1.0 and float(s[0]) == 1.0
+
+
 @pytest.mark.parametrize("layout,cap,dtype", [("reference", -1, torch.bfloat16), ("routed", -1, torch.bfloat16),
                                               ("routed", 40, torch.bfloat16), ("reference", -1, torch.float32)])
 def test_permute_fp8_bit_exact(layout, cap, dtype):

@@ -74,3 +74,26 @@ def test_swiglu_fwd_fp8_matches_loops():
     yl = O8.swiglu_fwd_fp8_loops(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets)
     assert torch.allclose(y, yl, rtol=0, atol=0) or (y - yl).abs().max().item() <= 2 ** -8 * yl.abs().max().item()
     assert y[6].abs().max().item() == 0.0 and hgu[6].abs().max().item() == 0.0
+
+
+def test_tiny_rows_quantize_to_zeros_not_nan():
+    """A row whose absmax is below 2^-118 (448 / absmax would overflow fp32 below ~1.3e-36, and 0 * inf is NaN)
+    is a zero row: scale 1, bytes +-0.  At 2^-118 itself the row keeps its own scale (448 * 2^118 is finite).
+    The rule it replaces -- any nonzero absmax gets its own scale -- turns such a row into NaN bytes."""
+    x = torch.zeros(4, 32)
+    x[0, :] = 1e-37
+    x[0, 3] = 0.0
+    x[1, :] = -2e-37
+    x[2, 5] = 2.0 ** -118
+    x[3, 7] = 2.0 ** -118 * 0.75
+    q, s = O8.quant_rows(x)
+    assert not bool(torch.isnan(O8.dequant(q, s)).any())
+    assert s[0].item() == 1.0 and s[1].item() == 1.0 and s[3].item() == 1.0
+    assert set(q[0].tolist()) == {0x00} and set(q[1].tolist()) == {0x80}
+    assert s[2].item() == pytest.approx(2.0 ** -118 / 448.0, rel=1e-6) and q[2, 5].item() == 0x7E
+    # planted mistake: a scale for every nonzero row
+    v = x[0:1]
+    inv = torch.full((1,), 448.0) / v.abs().amax(-1)
+    assert bool(torch.isinf(inv).all())
+    bad = (v * inv.unsqueeze(-1)).to(torch.float8_e4m3fn).float()
+    assert bool(torch.isnan(bad).any())

@@ -19,8 +19,9 @@ def test_record_layout_matches_the_library():
 
 def test_records_from_rows_decodes_counts_as_ints():
     row = torch.zeros(2, 16)
-    row[0, :12] = torch.tensor([3, 1.5, 2.25, 4.0, 1.0, 2, 6, 0.8, 0.125, 1.01, 0, 32])
-    row[1, 0] = 4
+    row[0, :12] = torch.tensor([0, 1.5, 2.25, 4.0, 1.0, 2, 6, 0.8, 0.125, 1.01, 0, 32])
+    row.view(torch.int32)[0, 0] = 3  # the step is stored as int32 bits
+    row.view(torch.int32)[1, 0] = 4
     recs = records_from_rows(row)
     assert recs[0]["step"] == 3 and isinstance(recs[0]["step"], int)
     assert recs[0]["expert_load_imbalance"] == 1.5 and recs[0]["router_z_loss"] == 2.25
@@ -35,7 +36,9 @@ def test_records_from_rows_decodes_counts_as_ints():
 
 def test_record_rejects_bad_arguments_without_gpu():
     lib = _lib.load()
-    assert lib.moe_telemetry_record(None, 0, 16, 2, 1.0, None, 0, None, None) == -1
+    assert lib.moe_telemetry_record(None, 0, 16, 2, 1.0, None, 0, None, 4, None) == -1
     assert "bad arguments" in _lib.last_error()
-    assert lib.moe_telemetry_record(None, 8, 16, 2, 1.0, None, 0, None, None) == -1
+    assert lib.moe_telemetry_record(None, 8, 16, 2, 1.0, None, 0, None, 0, None) == -1
+    assert "bad arguments" in _lib.last_error()
+    assert lib.moe_telemetry_record(None, 8, 16, 2, 1.0, None, 0, None, 4, None) == -1
     assert "null" in _lib.last_error()

@@ -99,11 +99,11 @@ def test_ring_keeps_the_newest_records_in_order():
 
 def test_record_is_capturable_in_a_graph():
     """Capture fails on any host synchronisation: the router forward (sync_profile=False) and the record
-    replay as one graph, and each replay rewrites the record."""
+    replay as one graph, and each replay appends a new record (the ring's cursor is on the device)."""
     say("[telemetry graph capture]")
     N, H, E, K = 128, 64, 8, 2
     router = MoERouter(H, E, top_k=K, sync_profile=False).to(dev())
-    tel = RoutingTelemetry(capacity=2)
+    tel = RoutingTelemetry(capacity=4)
     x = torch.randn(N, H, generator=torch.Generator().manual_seed(20)).to(dev())
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -114,11 +114,19 @@ def test_record_is_capturable_in_a_graph():
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         _idx, _w, cnt = router(x)
-        tel.record(router, step=1, capacity_factor=1.0)
-    for _ in range(3):
+        tel.record(router, capacity_factor=1.0)  # step = the record's ordinal
+    dead = -1
+    for i in range(3):
         g.replay()
         torch.cuda.synchronize()
-        rec = tel.ring[0].cpu()
-        assert int(rec[0].item()) == 1 and int(rec[11].item()) == N * K
-        assert int(rec[5].item()) == int((cnt.cpu() == 0).sum().item())
-    assert not math.isnan(float(tel.ring[0, 1].item()))
+        if i == 0:
+            dead = int((cnt.cpu() == 0).sum().item())
+    recs = tel.flush()
+    assert [r["step"] for r in recs] == [0, 1, 2]
+    for r in recs:
+        assert r["dispatched_slots"] == N * K and r["dead_expert_count"] == dead
+        assert not math.isnan(r["expert_load_imbalance"])
+    for _ in range(3):  # records 3..5 land in slots 3, 0, 1: across the wrap-around, oldest first
+        g.replay()
+    torch.cuda.synchronize()
+    assert [r["step"] for r in tel.flush()] == [3, 4, 5]
