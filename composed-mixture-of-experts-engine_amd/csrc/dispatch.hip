@@ -20,6 +20,7 @@
 // every backward reduce over the K slots of a token in registers (fp32) with
 // a single write, so no float atomics are involved anywhere.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -568,27 +569,24 @@ extern "C" size_t moe_plan_workspace(int64_t N, int64_t K, int64_t E) {
   return plan_ws(N, K, E).total;
 }
 
-extern "C" int moe_plan(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout,
-                        uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
-                        void* workspace, size_t ws_bytes, void* stream) {
+namespace moe {
+namespace {
+
+int plan_check(int64_t N, int64_t K, int64_t E, int layout, const int32_t* offsets, const int32_t* ndrop) {
   if (N < 0 || K < 1 || E < 1 || K > E || E > 1024 || K * E > 8192)
     return fail_arg("moe_plan: bad shape N=%lld K=%lld E=%lld", (long long)N, (long long)K, (long long)E);
   if (N * K > INT32_MAX / 2) return fail_arg("moe_plan: N*K too large");
   if (layout != 0 && layout != 1) return fail_arg("moe_plan: layout must be 0 (reference) or 1 (routed)");
   if (!offsets || !ndrop) return fail_arg("moe_plan: null offsets/ndrop");
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return 0;
+}
+
+// The plan proper, with its block tables in `ws` (plan_ws(N, K, E).total bytes; every table is written
+// before it is read, so ws needs no initialisation).
+int plan_run(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout, uint8_t* drop_out,
+             int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop, char* ws, hipStream_t s) {
   const int64_t M = N * K;
-  if (M == 0) {
-    MOE_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(256), 0, s, offsets, (int)(E + 1), 0);
-    MOE_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, s, ndrop, 1, 0);
-    return check_launch("moe_plan");
-  }
-  if (!idx || !row_slot || !slot_row) return fail_arg("moe_plan: null pointer argument");
-  if (capacity >= 0 && !drop_out) return fail_arg("moe_plan: capacity dropping needs drop_out");
   const PlanWs p = plan_ws(N, K, E);
-  if (ws_bytes < p.total || !workspace)
-    return set_error("moe_plan: workspace %zu < %zu bytes", ws_bytes, p.total), MOE_EWORKSPACE;
-  char* ws = static_cast<char*>(workspace);
   uint8_t* drop = capacity >= 0 ? drop_out : nullptr;
   if (drop) {
     if (int rc = grouping(s, kCapacity, idx, drop, M, (int)K, (int)E, (int)(K * E), capacity, p, ws, nullptr,
@@ -610,6 +608,83 @@ extern "C" int moe_plan(const int64_t* idx, int64_t N, int64_t K, int64_t E, int
                dim3(256), 0, s, offsets, (int)E, M, row_slot);
   }
   return check_launch("moe_plan");
+}
+
+// An empty plan (N * K == 0): zero offsets and drop count.
+int plan_empty(int64_t E, int32_t* offsets, int32_t* ndrop, hipStream_t s) {
+  MOE_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(256), 0, s, offsets, (int)(E + 1), 0);
+  MOE_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, s, ndrop, 1, 0);
+  return check_launch("moe_plan");
+}
+
+}  // namespace
+}  // namespace moe
+
+extern "C" int moe_plan(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout,
+                        uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
+                        void* workspace, size_t ws_bytes, void* stream) {
+  if (int rc = plan_check(N, K, E, layout, offsets, ndrop)) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (N * K == 0) return plan_empty(E, offsets, ndrop, s);
+  if (!idx || !row_slot || !slot_row) return fail_arg("moe_plan: null pointer argument");
+  if (capacity >= 0 && !drop_out) return fail_arg("moe_plan: capacity dropping needs drop_out");
+  const PlanWs p = plan_ws(N, K, E);
+  if (ws_bytes < p.total || !workspace)
+    return set_error("moe_plan: workspace %zu < %zu bytes", ws_bytes, p.total), MOE_EWORKSPACE;
+  return plan_run(idx, N, K, E, capacity, layout, drop_out, row_slot, slot_row, offsets, ndrop,
+                  static_cast<char*>(workspace), s);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free planner: the block tables live in `scratch`, a fixed device array of this library
+// (each GPU holds its own copy, from the library's load until the process ends).  In host code `scratch`
+// names a host-side stand-in, not device memory: its device address is looked up once per device with
+// hipGetSymbolAddress and only that address is handed to the kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[MOE_PLAN_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of the current device's `scratch` (looked up on the first call on that device).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error("moe_plan_noalloc: hipGetDevice: %s", hipGetErrorString(e)), (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return fail_arg("moe_plan_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error("moe_plan_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e)),
+             e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int moe_plan_noalloc(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout,
+                                uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets,
+                                int32_t* ndrop, void* stream) {
+  if (int rc = plan_check(N, K, E, layout, offsets, ndrop)) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (N * K == 0) return plan_empty(E, offsets, ndrop, s);
+  if (!idx || !row_slot || !slot_row) return fail_arg("moe_plan_noalloc: null pointer argument");
+  if (capacity >= 0 && !drop_out) return fail_arg("moe_plan_noalloc: capacity dropping needs drop_out");
+  const PlanWs p = plan_ws(N, K, E);
+  if (p.total > (size_t)MOE_PLAN_SCRATCH_BYTES)
+    return fail_arg("moe_plan_noalloc: N=%lld K=%lld E=%lld needs %zu bytes of block tables, more than the %d-byte "
+                    "scratch array (use moe_plan with a workspace)", (long long)N, (long long)K, (long long)E,
+                    p.total, MOE_PLAN_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  if (int rc = scratch_address(&ptr)) return rc;
+  return plan_run(idx, N, K, E, capacity, layout, drop_out, row_slot, slot_row, offsets, ndrop,
+                  static_cast<char*>(ptr), s);
 }
 
 extern "C" int moe_permute(const void* x, int64_t row_bytes, const int32_t* row_slot, const int32_t* offsets,

@@ -158,6 +158,20 @@ int moe_plan(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capaci
              uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
              void* workspace, size_t ws_bytes, void* stream);
 
+/* Allocation-free planner (no counterpart in the reference: for callers that cannot allocate device memory
+ * or take a workspace -- code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, outputs and errors as moe_plan without the workspace: the planner's block
+ * tables go to a fixed device array of MOE_PLAN_SCRATCH_BYTES inside the library, which each GPU the
+ * library runs on holds until the process ends.  Shapes whose tables exceed it (moe_plan_workspace(N, K, E)
+ * > MOE_PLAN_SCRATCH_BYTES; e.g. N*K > 2^21 slots at K*E = 1024 keys) are rejected with MOE_EINVAL.  The
+ * array needs no initialisation (every table is written before it is read) and keeps the last call's
+ * contents.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different
+ * streams, different host threads) race; serialise them.  Call it with the stream's device current. */
+#define MOE_PLAN_SCRATCH_BYTES (8 << 20)
+int moe_plan_noalloc(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout,
+                     uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
+                     void* stream);
+
 /* Permute (dispatch): xp[r] = x[row_slot[r] / K] for r < offsets[E]; rows are
  * row_bytes long (a multiple of 16).  Replaces flat[sort_order]
  * .repeat_interleave(K) (pkg/distributed/moe_layer.py L:318-319). */
