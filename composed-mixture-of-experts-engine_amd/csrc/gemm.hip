@@ -2,9 +2,16 @@
 //
 // One kernel template covers the six products of the expert FFN forward and
 // backward.  Each computes C[m, n] = sum_k A[m, k] B[n, k] on
-// v_mfma_f32_32x32x16_bf16 with 256x256 block tiles (8 waves of 128x64) and
-// a 2-stage LDS ring (128 KB) of 64-wide k slices filled by LDS-DMA
-// (global_load_lds_dwordx4), so no operand passes through VGPRs.  A 64-wide
+// v_mfma_f32_32x32x16_bf16 with 256x256 block tiles and a 2-stage LDS ring
+// (128 KB) of 64-wide k slices, in one of two forms:
+//   8 waves of 128x64, the ring filled by LDS-DMA (global_load_lds_dwordx4) so
+//     no operand passes through VGPRs (the backward products, whose operands
+//     are read with transposing LDS reads, and the fp8 forward);
+//   4 waves of 128x128, one per SIMD (the two bf16 forward products): a third
+//     fewer LDS fragment bytes per MFMA; the refill goes through registers two
+//     slices ahead, one 16-byte piece at a time between the MFMAs, with every
+//     MFMA slot of a k quarter carrying at most one fragment read and one
+//     refill piece (described at the loop).  A 64-wide
 // slice makes every row of a k-contiguous operand one whole 128-byte line:
 // each DMA instruction fetches 8 full lines, which moves about 1.5x the bytes
 // per cycle of half-line (32-wide) slices through the CU's load path, the
@@ -48,6 +55,7 @@
 //   dWd   dWd_e       = dy_e^T . act_e             A cols,     B cols,     G1, EPI0
 //   dW1   [dWg_e;dWu_e] = dh_e^T . xp_e            A cols,     B cols,     G1, EPI0
 #include <algorithm>
+#include <utility>
 
 #include "common.h"
 
@@ -432,6 +440,128 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       }
       wait_vmcnt<0>();
     }
+  } else if constexpr (NW == 4) {
+    static_assert(AMODE == 0 && BMODE == 0, "the 4-wave main loop takes k-contiguous operands");
+    // One wave per SIMD, 128x128 per wave.  The refill goes through registers two slices ahead: while slice
+    // kt is computed, each wave writes its share of slice kt+1 (loaded during slice kt-1) into the free LDS
+    // slot and loads its share of slice kt+2 into the same registers, one piece (16 bytes a lane) at a time
+    // between the MFMAs, so global loads, LDS writes and fragment reads are spread over the slice.  The loads
+    // are issued from asm, so the compiler does not drain them before the first LDS write: piece p of slice
+    // kt+1 was loaded NP loads before piece p of slice kt+2, and loads complete in order, so vmcnt(NP-1)
+    // before its write suffices (vmcnt(NP-1-p) once no new load follows).
+    constexpr int NP = 2 * QPW;  // pieces per wave per slice: A pieces 0..QPW-1, then B
+    u32x4 st[NP];
+    // source of piece p of slice kt; `full`: the slice lies inside the reduction range and on one side of
+    // b_split (no per-lane check)
+    auto gsrc = [&](int kt, int p, bool full) -> const uint16_t* {
+      const int k0 = kt * GBK;
+      if (p < QPW) {
+        const int q = p;
+        const int64_t step = AMODE != 1 ? (int64_t)k0 : (int64_t)k0 * g.lda;
+        if (full) return a_src[q] + step;
+        return (k0 + a_kl[q] < klen) ? a_src[q] + step : g_zero16;
+      }
+      const int q = p - QPW;
+      const int64_t bld = BMODE != 1 ? 1 : g.ldb;
+      if (full) {
+        if constexpr (BMODE == 1 && GROUP == 0) {
+          if (g.b_split > 0 && k0 >= g.b_split) return b_src2[q] + (int64_t)(k0 - g.b_split) * bld;
+        }
+        return b_src[q] + (int64_t)k0 * bld;
+      }
+      const int k = k0 + b_kl[q];
+      if (k >= klen) return g_zero16;
+      if constexpr (BMODE == 1 && GROUP == 0) {
+        if (g.b_split > 0 && k >= g.b_split) return b_src2[q] + (int64_t)(k0 - g.b_split) * bld;
+      }
+      return b_src[q] + (int64_t)k0 * bld;
+    };
+    auto slice_full = [&](int kt) {
+      const int k0 = kt * GBK;
+      bool f = k0 + GBK <= klen;
+      if constexpr (BMODE == 1 && GROUP == 0) f = f && !(g.b_split > 0 && k0 < g.b_split && k0 + GBK > g.b_split);
+      return f;
+    };
+    typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+    auto gload = [&](int kt, int p, bool full) {
+      st[p] = *reinterpret_cast<g_u32x4*>(reinterpret_cast<uintptr_t>(gsrc(kt, p, full)));
+    };
+    // ring units and tiles as the DMA path lays them out (piece q of wave wv fills bytes [1024 j, 1024 j + 1024),
+    // j = QPW wv + q, of its unit)
+    auto lwrite = [&](int kt, int p) {
+      const int op = p < QPW ? 0 : 1, q = p < QPW ? p : p - QPW;
+      __asm__ volatile("" ::: "memory");
+      *reinterpret_cast<u32x4*>(unit_ptr(2 * kt + op) + (QPW * wv + q) * 1024 + lane * 16) = st[p];
+      __asm__ volatile("" ::: "memory");
+    };
+    auto read_frag = [&](const uint8_t* as, const uint8_t* bs, int ks, int f, i16x8 (&fa)[MI], i16x8 (&fb)[NI]) {
+      if (f < MI) fa[f] = frag_rows(as, wm0 + f * 32, ks, lane);
+      else fb[f - MI] = frag_rows(bs, wn0 + (f - MI) * 32, ks, lane);
+    };
+    // One k quarter as 16 MFMA slots (mi-major), each followed by at most one fragment read of the next
+    // quarter (slots 0..MI+NI-1) and at most one refill piece (slots 8.., pieces [PLO, PHI)); sched_barrier
+    // keeps this order.  MODE 0: steady state (write slice kt+1, load full slice kt+2); 1: write, load with
+    // checks; 2: write only (no slice left to load); 3: no refill.
+    auto quarter = [&](auto mode_c, auto plo_c, auto phi_c, const i16x8 (&ca)[MI], const i16x8 (&cb)[NI],
+                       const uint8_t* nas, const uint8_t* nbs, int nks, bool read_next, i16x8 (&na)[MI],
+                       i16x8 (&nb)[NI], int kt, bool lfull) {
+      constexpr int MODE = decltype(mode_c)::value;
+      constexpr int PLO = decltype(plo_c)::value, PHI = decltype(phi_c)::value;
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        (([&] {
+           constexpr int i = I;
+           constexpr int mi = i / NI, ni = i % NI;
+           acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, ca[mi]), __builtin_bit_cast(bf16x8, cb[ni]), acc[mi][ni]);
+           __builtin_amdgcn_sched_barrier(0);
+           if constexpr (i < MI + NI) {
+             if (read_next) read_frag(nas, nbs, nks, i, na, nb);
+           }
+           constexpr int p = PLO + (i - 8);
+           if constexpr (MODE < 3 && i >= 8 && p < PHI) {
+             lwrite(kt + 1, p);
+             if constexpr (MODE == 0) gload(kt + 2, p, true);
+             else if constexpr (MODE == 1) gload(kt + 2, p, lfull);
+           }
+           __builtin_amdgcn_sched_barrier(0);
+         }()), ...);
+      }(std::make_integer_sequence<int, MI * NI>{});
+    };
+    constexpr int PB1 = (NP + 2) / 3, PB2 = (2 * NP + 2) / 3;
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, PB1>;
+    using P2 = std::integral_constant<int, PB2>;
+    using P3 = std::integral_constant<int, NP>;
+    i16x8 fa0[MI], fb0[NI], fa1[MI], fb1[NI];
+    auto slice = [&](auto mode_c, int kt) {
+      const uint8_t* const ca = unit_ptr(2 * kt);
+      const uint8_t* const cb = unit_ptr(2 * kt + 1);
+      const bool lfull = kt + 2 < nk ? slice_full(kt + 2) : true;
+      quarter(mode_c, P0{}, P1{}, fa0, fb0, ca, cb, 1, true, fa1, fb1, kt, lfull);
+      quarter(mode_c, P1{}, P2{}, fa1, fb1, ca, cb, 2, true, fa0, fb0, kt, lfull);
+      quarter(mode_c, P2{}, P3{}, fa0, fb0, ca, cb, 3, true, fa1, fb1, kt, lfull);
+      wait_vmcnt_lgkm0<63>();  // this wave's LDS writes of slice kt+1 and reads of slice kt are done
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      quarter(std::integral_constant<int, 3>{}, P3{}, P3{}, fa1, fb1, unit_ptr(2 * kt + 2), unit_ptr(2 * kt + 3), 0,
+              kt + 1 < nk, fa0, fb0, kt, true);
+    };
+    if (nk > 0) {
+      for (int p = 0; p < NP; ++p) gload(0, p, slice_full(0));
+      for (int p = 0; p < NP; ++p) lwrite(0, p);
+      if (nk > 1) {
+        for (int p = 0; p < NP; ++p) gload(1, p, slice_full(1));
+      }
+      __syncthreads();
+      frags(unit_ptr(0), unit_ptr(1), 0, fa0, fb0);
+      int kt = 0;
+      // steady state: slice kt+2 <= nk-2 is full (only the last slice of the reduction can be partial,
+      // and b_split falls on a slice boundary whenever every slice is full)
+      for (; kt + 3 < nk && slice_full(kt + 2); ++kt) slice(std::integral_constant<int, 0>{}, kt);
+      for (; kt + 2 < nk; ++kt) slice(std::integral_constant<int, 1>{}, kt);
+      if (kt + 1 < nk) slice(std::integral_constant<int, 2>{}, kt++);
+      if (kt < nk) slice(std::integral_constant<int, 3>{}, kt);
+    }
+    wait_vmcnt<0>();
   } else if (nk > 0) {
     issue_unit(0);
     issue_unit(1);
@@ -673,12 +803,10 @@ int launch(const char* name, hipStream_t s, const GemmArgs& a, int64_t R) {
 }
 
 constexpr int kTileBM = GBM;
-// wave layout per product (8: 8 waves of 128x64, 4: 4 waves of 128x128)
-#ifndef MOE_GEMM_NW
-#define MOE_GEMM_NW 8
-#endif
-constexpr int kNW_fwd1 = MOE_GEMM_NW, kNW_fwd2 = MOE_GEMM_NW, kNW_dact = MOE_GEMM_NW, kNW_dxp = MOE_GEMM_NW,
-              kNW_dwd = MOE_GEMM_NW, kNW_dw1 = MOE_GEMM_NW;  // the row-grouped tile prefix is computed with the kernel's BM
+// Wave layout per product: 4 waves of 128x128 (one per SIMD; register-staged refill two slices ahead) for the
+// forward products, whose operands are both k-contiguous; 8 waves of 128x64 (LDS-DMA refill) for the
+// backward products and the fp8 forward.  The row-grouped tile prefix is computed with the kernels' BM.
+constexpr int kNW_fwd1 = 4, kNW_fwd2 = 4, kNW_dact = 8, kNW_dxp = 8, kNW_dwd = 8, kNW_dw1 = 8, kNW_fp8 = 8;
 }  // namespace
 }  // namespace moe
 
@@ -782,7 +910,7 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
   a.ldc = F;
   a.N = (int)(2 * F);
   a.K = (int)(H / 2);
-  if (int rc = launch<2, 2, 0, 1, kNW_fwd1>("k_gemm_swiglu_fwd1_fp8", s, a, R)) return rc;
+  if (int rc = launch<2, 2, 0, 1, kNW_fp8>("k_gemm_swiglu_fwd1_fp8", s, a, R)) return rc;
   // act -> e4m3 with a scale per row, then fwd2: y = (actq sact) . (Wd sd)^T
   // (rows past offsets[E] are never read by the down projection and are not quantized)
   if (int rc = quant_rows_fp8(act, MOE_BF16, R, F, F, actq, sact, offsets + E, s)) return rc;
@@ -802,7 +930,7 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
   b.ldc = H;
   b.N = (int)H;
   b.K = (int)(F / 2);
-  return launch<2, 2, 0, 0, kNW_fwd2>("k_gemm_swiglu_fwd2_fp8", s, b, R);
+  return launch<2, 2, 0, 0, kNW_fp8>("k_gemm_swiglu_fwd2_fp8", s, b, R);
 }
 
 extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* hgu, const void* w_gate,
