@@ -2,15 +2,17 @@
 //
 // Planner: every index structure of the MoE layer is a stable grouping of a
 // sequence of items by an integer key -- the rank of item i among earlier
-// items with the same key.  Three passes, all deterministic:
-//   count  per block of IB items, an LDS histogram (integer atomics, order
-//          independent) -> counts[block][key]
-//   scan   per key, exclusive prefix over blocks; then exclusive prefix over
-//          keys -> key offsets
-//   rank   one wave per block walks its items in order, 64 at a time; lanes
-//          with equal keys are found with log2(nkeys) ballots (bit-split
-//          match), rank-in-chunk = popcount of the lower matching lanes, and a
-//          per-key running count in LDS carries the order across chunks.
+// items with the same key.  Inside one block the items are split into one
+// contiguous part per wave; each wave loads its part's keys into registers
+// (one memory round trip), counts them per key (lanes with equal keys are
+// found with log2(nkeys) ballots, a bit-split match), the per-wave counts are
+// prefixed over waves, and a second walk over the registers gives each item
+// its rank: the wave's running count + the popcount of the lower matching
+// lanes.  Small plans run in one block; larger ones in three launches per
+// grouping, all deterministic:
+//   count  per block of IB items, an LDS histogram -> counts[key][block]
+//   scan   one wave per key: exclusive prefix over blocks, key totals
+//   rank   per block: key offsets (prefix of the totals), in-block ranks
 // Modes (the key of item i):
 //   CAPACITY  items = slots t*K+k, key = k*E + idx[t,k]   -> drop = rank >= capacity
 //   REFSORT   items = tokens t,    key = idx[t,0]         -> stable sort of column 0
@@ -20,6 +22,7 @@
 // every backward reduce over the K slots of a token in registers (fp32) with
 // a single write, so no float atomics are involved anywhere.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -33,72 +36,159 @@ constexpr int kPlanIB = 2048;  // items per planner block
 // outside the planner's tables (the router only produces ids in range).
 __device__ __forceinline__ int clamp_e(int64_t v, int E) { return (int)min(max(v, (int64_t)0), (int64_t)(E - 1)); }
 
-__device__ __forceinline__ int plan_key(int mode, const int64_t* __restrict__ idx, int64_t i, int K, int E) {
-  if (mode == kCapacity) return (int)(i % K) * E + clamp_e(idx[i], E);
-  if (mode == kRefSort) return clamp_e(idx[i * K], E);
-  return clamp_e(idx[i], E);
+__host__ __device__ inline int nbits_of(int nkeys) {
+  int b = 0;
+  while ((1 << b) < nkeys) ++b;
+  return b;
 }
 
-__device__ __forceinline__ bool plan_valid(int mode, const uint8_t* __restrict__ drop, int64_t i) {
-  return !(mode == kRouted && drop != nullptr && drop[i]);
+// ---------------------------------------------------------------------------
+// Stable grouping inside one 1024-thread block.  The items of a range are split into nwr contiguous parts,
+// one per wave (waves past nwr idle: nwr shrinks with the key count so the per-wave key counts fit in LDS).
+//   pass 1  each wave walks its part in chunks of 64 and counts its items per key: lanes with equal keys
+//           are found with log2(nkeys) ballots (bit-split match); the lowest lane of each key group adds
+//           the group's size to cnt[w][key] (one writer per key per chunk: no atomics)
+//   prefix  per key, exclusive prefix of cnt[.][key] over the waves (tot[key] = the range's total)
+//   pass 2  each wave walks its part again: an item's rank among the range's items of its key is
+//           cnt[w][key] (running) + its rank among the equal-keyed lanes of its chunk
+// Ranks therefore follow the item order exactly, and the result is independent of timing.
+// ---------------------------------------------------------------------------
+constexpr int kPlanNT = 1024;            // threads of a planner block (16 waves)
+constexpr int kPlanSmall = 16384;        // largest item count the single-block planner takes
+constexpr int kPlanCntInts = 24576;      // LDS ints of the per-wave key counts (96 KB)
+
+__host__ __device__ constexpr int plan_nwr(int nkeys) {
+  int w = 16;
+  while (w > 1 && w * nkeys > kPlanCntInts) w >>= 1;
+  return w;
 }
 
-__global__ __launch_bounds__(256) void k_plan_count(int mode, const int64_t* __restrict__ idx,
-                                                    const uint8_t* __restrict__ drop, int64_t M, int K, int E,
-                                                    int nkeys, int* __restrict__ counts, int* __restrict__ ndrop) {
-  extern __shared__ int hist[];
-  for (int q = threadIdx.x; q < nkeys; q += blockDim.x) hist[q] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0 && ndrop != nullptr && mode == kCapacity) ndrop[0] = 0;
-  __syncthreads();
-  const int64_t beg = (int64_t)blockIdx.x * kPlanIB;
-  const int64_t end = min(M, beg + kPlanIB);
-  for (int64_t i = beg + threadIdx.x; i < end; i += blockDim.x)
-    if (plan_valid(mode, drop, i)) atomicAdd(&hist[plan_key(mode, idx, i, K, E)], 1);
-  __syncthreads();
-  for (int q = threadIdx.x; q < nkeys; q += blockDim.x) counts[(int64_t)blockIdx.x * nkeys + q] = hist[q];
+__device__ __forceinline__ uint64_t key_match(bool valid, int key, int nbits) {
+  uint64_t m = __ballot(valid);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool b = (key >> bit) & 1;
+    const uint64_t bm = __ballot(valid && b);
+    m &= b ? bm : ~bm;
+  }
+  return valid ? m : 0ull;
 }
 
-// base[b][key] = sum_{b' < b} counts[b'][key]; totals[key] = sum_b counts[b][key].
-// Block = 16 keys x 16 block-segments.
-__global__ __launch_bounds__(256) void k_plan_scan_blocks(const int* __restrict__ counts, int nblk, int nkeys,
-                                                          int* __restrict__ base, int* __restrict__ totals) {
-  __shared__ int ss[16][16];
-  const int kl = threadIdx.x & 15;
-  const int seg = threadIdx.x >> 4;
-  const int key = blockIdx.x * 16 + kl;
-  const int bps = (nblk + 15) / 16;
-  const int b0 = min(nblk, seg * bps);
-  const int b1 = min(nblk, b0 + bps);
-  int sum = 0;
-  if (key < nkeys)
-    for (int b = b0; b < b1; ++b) sum += counts[(int64_t)b * nkeys + key];
-  ss[seg][kl] = sum;
-  __syncthreads();
-  if (key < nkeys) {
-    int run = 0;
-    for (int s = 0; s < seg; ++s) run += ss[s][kl];
-    for (int b = b0; b < b1; ++b) {
-      base[(int64_t)b * nkeys + key] = run;
-      run += counts[(int64_t)b * nkeys + key];
-    }
-    if (seg == 15) totals[key] = run;
+// Per-mode keys (items: slots t*K+k for CAPACITY and ROUTED, tokens t for REFSORT).  Item i's expert id is read
+// at idx[i * stride] (and ROUTED's drop flag at drop[i]); key() turns them into the item's key, -1 for an
+// item without one (a dropped slot).
+struct PlanKeys {
+  const int64_t* idx;
+  const uint8_t* drop;  // ROUTED: dropped slots have no key (null: none dropped)
+  int K, E;
+  __device__ __forceinline__ int64_t stride(int mode) const { return mode == kRefSort ? K : 1; }
+  __device__ __forceinline__ int key(int mode, int64_t i, int64_t e, int d) const {
+    const int ce = clamp_e(e, E);
+    if (mode == kCapacity) return ((int)i % K) * E + ce;  // i < 2^31 (N*K is bounded on the host)
+    return (mode == kRouted && d) ? -1 : ce;
+  }
+};
+
+// A wave's part of a range, its keys loaded into registers first (one round of loads for both passes): chunk c
+// of the part covers items lo + 64 c + lane; key[c] = the item's key, -1 for an item without one (ROUTED: a
+// dropped slot), -2 past the part.
+constexpr int kPlanCh = 16;  // chunks a wave holds (the part of a wave is at most 64 * kPlanCh items)
+// a multi-block rank pass splits kPlanIB items over plan_nwr(nkeys) waves; nkeys <= 8192 (K*E)
+static_assert(plan_nwr(8192) * 64 * kPlanCh >= kPlanIB, "a rank block's items must fit its waves");
+static_assert(8192 <= 8 * kPlanNT, "a rank block's threads hold at most 8 keys each");
+
+struct WaveKeys {
+  int key[kPlanCh];
+  int64_t lo;
+  int nch;
+};
+
+// Every load is issued before any key is formed (clamped addresses: lanes past the range re-read its last
+// item), so the part's keys cost one memory round trip.
+__device__ __forceinline__ void load_keys(WaveKeys& wk, int64_t beg, int64_t end, int nwr, int w, int lane,
+                                          const PlanKeys& pk, int mode) {
+  const int64_t part = (((end - beg) + (int64_t)nwr * 64 - 1) / ((int64_t)nwr * 64)) * 64;
+  wk.lo = beg + (int64_t)w * part;
+  const int64_t hi = min(end, wk.lo + part);
+  wk.nch = hi > wk.lo ? (int)((hi - wk.lo + 63) / 64) : 0;
+  const int64_t st = pk.stride(mode);
+  const uint8_t* dp = mode == kRouted ? pk.drop : nullptr;
+  int64_t e[kPlanCh];
+  int d[kPlanCh];
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) e[c] = pk.idx[min(wk.lo + 64 * c + lane, end - 1) * st];
+  if (dp) {
+#pragma unroll
+    for (int c = 0; c < kPlanCh; ++c) d[c] = dp[min(wk.lo + 64 * c + lane, end - 1)];
+  } else {
+#pragma unroll
+    for (int c = 0; c < kPlanCh; ++c) d[c] = 0;
+  }
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) {
+    const int64_t i = wk.lo + 64 * c + lane;
+    wk.key[c] = (c < wk.nch && i < hi) ? pk.key(mode, i, e[c], d[c]) : -2;
   }
 }
 
-// key_off[0..nkeys] = exclusive prefix of totals (one block of 1024 threads).
-__global__ __launch_bounds__(1024) void k_plan_scan_keys(const int* __restrict__ totals, int nkeys,
-                                                         int* __restrict__ key_off) {
-  __shared__ int part[1024];
+// pass 1 (wave w < nwr): cnt[w * nkeys + key] = items of the wave's part with that key
+__device__ __forceinline__ void group_count(const WaveKeys& wk, int w, int lane, int nkeys, int nbits, int* cnt) {
+  const uint64_t lt = lane ? ((~0ull) >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) {
+    if (c < wk.nch) {  // wave-uniform
+      const int key = wk.key[c];
+      const bool valid = key >= 0;
+      const uint64_t m = key_match(valid, key, nbits);
+      if (valid && (m & lt) == 0) cnt[w * nkeys + key] += __popcll(m);
+    }
+  }
+}
+
+// prefix: cnt[w][key] <- sum_{w' < w} cnt[w'][key]; tot[key] <- sum over all waves (tot may be null)
+__device__ __forceinline__ void group_prefix(int nwr, int nkeys, int* cnt, int* tot) {
+  for (int key = threadIdx.x; key < nkeys; key += blockDim.x) {
+    int run = 0;
+    for (int w = 0; w < nwr; ++w) {
+      const int v = cnt[w * nkeys + key];
+      cnt[w * nkeys + key] = run;
+      run += v;
+    }
+    if (tot) tot[key] = run;
+  }
+}
+
+// pass 2 (wave w < nwr): out(i, key, rank) for each item with a key, skip(i) for each item without one
+template <class Out, class Skip>
+__device__ __forceinline__ void group_rank(const WaveKeys& wk, int w, int lane, int nkeys, int nbits, int* cnt,
+                                           Out out, Skip skip) {
+  const uint64_t lt = lane ? ((~0ull) >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) {
+    if (c < wk.nch) {  // wave-uniform
+      const int key = wk.key[c];
+      const int64_t i = wk.lo + 64 * c + lane;
+      const bool valid = key >= 0;
+      const uint64_t m = key_match(valid, key, nbits);
+      const int run = valid ? cnt[w * nkeys + key] : 0;
+      if (valid) out(i, key, run + __popcll(m & lt));
+      else if (key == -1) skip(i);
+      // the running count moves on only after every lane of the key group has read it (a wave's LDS
+      // operations complete in order)
+      if (valid && (m & lt) == 0) cnt[w * nkeys + key] = run + __popcll(m);
+    }
+  }
+}
+
+// exclusive prefix of tot[0..n) into off[0..n] (off[n] = total) by one 1024-thread block; part: LDS [1024]
+__device__ __forceinline__ void block_excl_scan(const int* tot, int n, int* off, int* part) {
   const int tid = threadIdx.x;
-  const int per = (nkeys + 1023) / 1024;
-  const int k0 = min(nkeys, tid * per);
-  const int k1 = min(nkeys, k0 + per);
-  int s = 0;
-  for (int k = k0; k < k1; ++k) s += totals[k];
-  part[tid] = s;
+  const int per = (n + kPlanNT - 1) / kPlanNT;
+  const int k0 = min(n, tid * per), k1 = min(n, k0 + per);
+  int sum = 0;
+  for (int k = k0; k < k1; ++k) sum += tot[k];
+  part[tid] = sum;
   __syncthreads();
-  // Hillis-Steele inclusive scan over 1024 partials
-  for (int o = 1; o < 1024; o <<= 1) {
+  for (int o = 1; o < kPlanNT; o <<= 1) {
     const int v = tid >= o ? part[tid - o] : 0;
     __syncthreads();
     part[tid] += v;
@@ -106,69 +196,277 @@ __global__ __launch_bounds__(1024) void k_plan_scan_keys(const int* __restrict__
   }
   int run = tid ? part[tid - 1] : 0;
   for (int k = k0; k < k1; ++k) {
-    key_off[k] = run;
-    run += totals[k];
+    off[k] = run;
+    run += tot[k];
   }
-  if (tid == 1023) key_off[nkeys] = part[1023];
+  if (tid == kPlanNT - 1) off[n] = part[kPlanNT - 1];
+  __syncthreads();
 }
 
-__global__ __launch_bounds__(64) void k_plan_rank(int mode, const int64_t* __restrict__ idx,
-                                                  uint8_t* __restrict__ drop, int64_t M, int K, int E, int nkeys,
-                                                  int nbits, const int* __restrict__ base,
-                                                  const int* __restrict__ key_off, int64_t capacity,
-                                                  int* __restrict__ row_slot, int* __restrict__ slot_row,
-                                                  int* __restrict__ ndrop) {
-  extern __shared__ int run[];
-  const int lane = threadIdx.x;
-  for (int q = lane; q < nkeys; q += 64) run[q] = 0;
+__device__ __forceinline__ int block_sum(int v, int* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
   __syncthreads();
-  const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-  const int64_t beg = (int64_t)blockIdx.x * kPlanIB;
-  const int64_t end = min(M, beg + kPlanIB);
-  int dropped = 0;
-  for (int64_t c0 = beg; c0 < end; c0 += 64) {
-    const int64_t i = c0 + lane;
-    const bool active = i < end;
-    const bool valid = active && plan_valid(mode, drop, i);
-    const int key = valid ? plan_key(mode, idx, i, K, E) : 0;
-    uint64_t m = __ballot(valid);
-    for (int bit = 0; bit < nbits; ++bit) {
-      const bool b = (key >> bit) & 1;
-      const uint64_t bm = __ballot(valid && b);
-      m &= b ? bm : ~bm;
-    }
-    if (!valid) m = 0;
-    const int rank = __popcll(m & lt);
-    const int cnt = __popcll(m);
-    const int r = valid ? run[key] : 0;
-    __syncthreads();
-    if (valid && (m & lt) == 0) run[key] = r + cnt;
-    __syncthreads();
-    if (!active) continue;
-    if (!valid) {  // ROUTED with a dropped slot
-      slot_row[i] = -1;
-      continue;
-    }
-    const int pin = base[(int64_t)blockIdx.x * nkeys + key] + r + rank;  // rank among all items of this key
-    if (mode == kCapacity) {
-      const bool d = (int64_t)pin >= capacity;
-      drop[i] = d ? 1 : 0;
-      dropped += d ? 1 : 0;
-    } else if (mode == kRefSort) {
-      const int j = key_off[key] + pin;  // position of token i in the stable sort of column 0
-      for (int k = 0; k < K; ++k) {
-        row_slot[(int64_t)j * K + k] = (int)(i * K + k);
-        slot_row[i * K + k] = j * K + k;
-      }
-    } else {
-      const int row = key_off[key] + pin;
-      row_slot[row] = (int)i;
-      slot_row[i] = row;
+  int t = 0;
+  for (int q = 0; q < (int)(blockDim.x >> 6); ++q) t += red[q];
+  __syncthreads();
+  return t;
+}
+
+// Largest item count of one wave-split range (the part of a wave holds at most kPlanCh chunks of 64).
+__host__ __device__ inline int64_t plan_range_max(int nkeys) { return (int64_t)plan_nwr(nkeys) * 64 * kPlanCh; }
+
+// ints of the per-wave key count table of the single-block planner (its capacity and layout groupings)
+__host__ __device__ inline int plan_small_cnt(int nk_max, int E) {
+  const int a = plan_nwr(nk_max) * nk_max, b = plan_nwr(E) * E;
+  return a > b ? a : b;
+}
+
+// The single-block planner takes N*K <= kPlanSmall items when every grouping's range fits its waves.
+__host__ __device__ inline bool plan_small_ok(int64_t M, int nk_max, int E) {
+  return M <= kPlanSmall && M <= plan_range_max(nk_max) && M <= plan_range_max(E);
+}
+
+// Rank callbacks of the layouts, shared by the single-block and the multi-block planner.  koff: key offsets;
+// bbase(key): the key's items in earlier blocks (0 in the single-block planner).
+struct RefOut {  // REFSORT: token t at position j of the stable sort of column 0 takes rows j*K .. j*K+K-1
+  int K;
+  int* row_slot;
+  int* slot_row;
+  __device__ __forceinline__ void operator()(int64_t t, int64_t j) const {
+    for (int k = 0; k < K; ++k) {
+      row_slot[j * K + k] = (int)(t * K + k);
+      slot_row[t * K + k] = (int)(j * K + k);
     }
   }
+};
+
+// The whole plan in one block, for plan_small_ok(N*K): capacity drops (optional), then the reference or the
+// routed row layout, all tables in LDS.  LDS: cnt [plan_small_cnt] + tot [nkeys] + off [nkeys + 1] +
+// part [1024] + red [16] ints, nkeys = K*E with drops, E otherwise.
+__global__ __launch_bounds__(kPlanNT) void k_plan_small(const int64_t* __restrict__ idx, int N, int K, int E,
+                                                        int64_t capacity, int layout, uint8_t* __restrict__ drop,
+                                                        int* __restrict__ row_slot, int* __restrict__ slot_row,
+                                                        int* __restrict__ offsets, int* __restrict__ ndrop) {
+  extern __shared__ int lds[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t M = (int64_t)N * K;
+  const int nk_max = capacity >= 0 ? K * E : E;
+  int* cnt = lds;
+  int* tot = cnt + plan_small_cnt(nk_max, E);
+  int* off = tot + nk_max;
+  int* part = off + nk_max + 1;
+  int* red = part + kPlanNT;
+  PlanKeys pk{idx, capacity >= 0 ? drop : nullptr, K, E};
+  int dropped = 0;
+  WaveKeys wk;
+  if (capacity >= 0) {
+    const int nkeys = K * E, nwr = plan_nwr(nkeys), nbits = nbits_of(nkeys);
+    if (w < nwr) load_keys(wk, 0, M, nwr, w, lane, pk, kCapacity);
+    for (int q = threadIdx.x; q < nwr * nkeys; q += kPlanNT) cnt[q] = 0;
+    __syncthreads();
+    if (w < nwr) group_count(wk, w, lane, nkeys, nbits, cnt);
+    __syncthreads();
+    group_prefix(nwr, nkeys, cnt, nullptr);
+    __syncthreads();
+    if (w < nwr)
+      group_rank(wk, w, lane, nkeys, nbits, cnt,
+                 [&](int64_t i, int, int rank) {
+                   const bool d = (int64_t)rank >= capacity;
+                   drop[i] = d ? 1 : 0;
+                   dropped += d ? 1 : 0;
+                 },
+                 [](int64_t) {});
+    __syncthreads();  // the drops are visible to the whole block (workgroup-scope fence)
+  }
+  const int total_dropped = block_sum(dropped, red);
+  if (threadIdx.x == 0) ndrop[0] = total_dropped;
+  const int nkeys = E, nwr = plan_nwr(E), nbits = nbits_of(E);
+  const int64_t nitems = layout == 0 ? N : M;
+  if (w < nwr) load_keys(wk, 0, nitems, nwr, w, lane, pk, layout == 0 ? kRefSort : kRouted);
+  for (int q = threadIdx.x; q < nwr * nkeys; q += kPlanNT) cnt[q] = 0;
+  __syncthreads();
+  if (w < nwr) group_count(wk, w, lane, nkeys, nbits, cnt);
+  __syncthreads();
+  group_prefix(nwr, nkeys, cnt, tot);
+  __syncthreads();
+  block_excl_scan(tot, nkeys, off, part);
+  if (layout == 0) {
+    const RefOut ro{K, row_slot, slot_row};
+    if (w < nwr)
+      group_rank(wk, w, lane, nkeys, nbits, cnt, [&](int64_t t, int key, int rank) { ro(t, off[key] + rank); },
+                 [](int64_t) {});
+    const int64_t chunk = max((int64_t)1, M / E);  // E equal chunks; rows past E*chunk are never computed
+    for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = (int)min((int64_t)e * chunk, M);
+  } else {
+    if (w < nwr)
+      group_rank(wk, w, lane, nkeys, nbits, cnt,
+                 [&](int64_t i, int key, int rank) {
+                   const int row = off[key] + rank;
+                   row_slot[row] = (int)i;
+                   slot_row[i] = row;
+                 },
+                 [&](int64_t i) { slot_row[i] = -1; });
+    for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = off[e];
+    for (int64_t r = off[E] + threadIdx.x; r < M; r += kPlanNT) row_slot[r] = -1;  // no row past the kept ones
+  }
+}
+
+// Multi-block path, per grouping: count -> scan -> rank.
+// Count: per block of kPlanIB items, counts[key * nblk + b] (key-major, so that the scan reads each key's
+// block counts contiguously); the block's keys are loaded before any is counted.  Block 0 zeroes ndrop in
+// the first grouping of a plan.
+constexpr int kPlanCountNT = 256;
+__global__ __launch_bounds__(kPlanCountNT) void k_plan_count(int mode, PlanKeys pk, int64_t M, int nkeys, int nblk,
+                                                             int* __restrict__ counts, int* __restrict__ ndrop,
+                                                             int zero_ndrop) {
+  extern __shared__ int hist[];
+  constexpr int PER = kPlanIB / kPlanCountNT;
+  const int64_t beg = (int64_t)blockIdx.x * kPlanIB;
+  const int64_t end = min(M, beg + kPlanIB);
+  const int64_t st = pk.stride(mode);
+  const uint8_t* dp = mode == kRouted ? pk.drop : nullptr;
+  int64_t e[PER];
+  int d[PER], key[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) e[j] = pk.idx[min(beg + j * kPlanCountNT + threadIdx.x, end - 1) * st];
+  if (dp) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) d[j] = dp[min(beg + j * kPlanCountNT + threadIdx.x, end - 1)];
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) d[j] = 0;
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t i = beg + j * kPlanCountNT + threadIdx.x;
+    key[j] = i < end ? pk.key(mode, i, e[j], d[j]) : -1;
+  }
+  for (int q = threadIdx.x; q < nkeys; q += kPlanCountNT) hist[q] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0 && zero_ndrop) ndrop[0] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (key[j] >= 0) atomicAdd(&hist[key[j]], 1);
+  __syncthreads();
+  for (int q = threadIdx.x; q < nkeys; q += kPlanCountNT) counts[(int64_t)q * nblk + blockIdx.x] = hist[q];
+}
+
+// Scan: one wave per key, base[key * nblk + b] = the key's items in blocks before b, key_tot[key] = its total.
+// The block counts are loaded 256 at a time before they are scanned.
+__global__ __launch_bounds__(256) void k_plan_scan(const int* __restrict__ counts, int nblk, int nkeys,
+                                                   int* __restrict__ base, int* __restrict__ key_tot) {
+  const int lane = threadIdx.x & 63;
+  const int key = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (key >= nkeys) return;
+  const int* c = counts + (int64_t)key * nblk;
+  int* bo = base + (int64_t)key * nblk;
+  int run = 0;
+  for (int b0 = 0; b0 < nblk; b0 += 256) {
+    int v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = b0 + 64 * j + lane;
+      v[j] = b < nblk ? c[b] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int incl = v[j];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+      }
+      const int b = b0 + 64 * j + lane;
+      if (b < nblk) bo[b] = run + incl - v[j];
+      run += __shfl(incl, 63);
+    }
+  }
+  if (lane == 0) key_tot[key] = run;
+}
+
+// Rank: one 1024-thread block per kPlanIB items.  The block loads its keys and its column of the block bases,
+// forms kb[key] = key offset (exclusive prefix of key_tot; none for CAPACITY, whose ranks are per key) + the
+// key's items in earlier blocks in LDS meanwhile, ranks its items inside the block (16-wave grouping) and adds
+// kb.  Block 0 (no earlier blocks) writes the layout's offsets; ROUTED pads row_slot past the kept rows with
+// -1 (spread over the blocks).  CAPACITY with counts_next: also the block's kept slots per expert, the count
+// pass of the ROUTED grouping that follows (same items, same blocks).
+// LDS: cnt [nwr * nkeys] + kb [nkeys + 1] + part [1024] + red [16] + hist [E] ints.
+constexpr int kPlanKPT = 8;  // keys per thread of a rank block (nkeys <= 8192)
+__global__ __launch_bounds__(kPlanNT) void k_plan_rank(int mode, PlanKeys pk, int64_t nitems, int64_t M, int nkeys,
+                                                       int nblk, const int* __restrict__ base,
+                                                       const int* __restrict__ key_tot, int64_t capacity,
+                                                       uint8_t* __restrict__ drop, int* __restrict__ row_slot,
+                                                       int* __restrict__ slot_row, int* __restrict__ offsets,
+                                                       int* __restrict__ ndrop, int* __restrict__ counts_next) {
+  extern __shared__ int lds[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = pk.K, E = pk.E;
+  const int nwr = plan_nwr(nkeys), nbits = nbits_of(nkeys);
+  int* cnt = lds;
+  int* kb = cnt + nwr * nkeys;
+  int* part = kb + nkeys + 1;
+  int* red = part + kPlanNT;
+  int* hist = red + 16;
+  const int b = blockIdx.x;
+  WaveKeys wk;
+  if (w < nwr)
+    load_keys(wk, (int64_t)b * kPlanIB, min(nitems, (int64_t)(b + 1) * kPlanIB), nwr, w, lane, pk, mode);
+  int bv[kPlanKPT];
+#pragma unroll
+  for (int j = 0; j < kPlanKPT; ++j) bv[j] = base[(int64_t)min((int)threadIdx.x + j * kPlanNT, nkeys - 1) * nblk + b];
+  for (int q = threadIdx.x; q < nwr * nkeys; q += kPlanNT) cnt[q] = 0;
+  if (counts_next)
+    for (int q = threadIdx.x; q < E; q += kPlanNT) hist[q] = 0;
+  if (mode == kCapacity) __syncthreads();
+  else block_excl_scan(key_tot, nkeys, kb, part);  // ends with a barrier
+#pragma unroll
+  for (int j = 0; j < kPlanKPT; ++j) {
+    const int key = threadIdx.x + j * kPlanNT;
+    if (key < nkeys) kb[key] = (mode == kCapacity ? 0 : kb[key]) + bv[j];
+  }
+  if (w < nwr) group_count(wk, w, lane, nkeys, nbits, cnt);
+  __syncthreads();
+  group_prefix(nwr, nkeys, cnt, nullptr);
+  __syncthreads();  // cnt prefixed, kb complete
   if (mode == kCapacity) {
-    dropped = wave_sum(dropped);
-    if (lane == 0 && dropped) atomicAdd(ndrop, dropped);
+    int dropped = 0;
+    if (w < nwr)
+      group_rank(wk, w, lane, nkeys, nbits, cnt,
+                 [&](int64_t i, int key, int rank) {
+                   const bool d = (int64_t)(kb[key] + rank) >= capacity;
+                   drop[i] = d ? 1 : 0;
+                   dropped += d ? 1 : 0;
+                   if (counts_next && !d) atomicAdd(&hist[key % E], 1);
+                 },
+                 [](int64_t) {});
+    const int t = block_sum(dropped, red);  // its barriers also complete the hist updates
+    if (threadIdx.x == 0 && t) atomicAdd(ndrop, t);
+    if (counts_next)
+      for (int q = threadIdx.x; q < E; q += kPlanNT) counts_next[(int64_t)q * nblk + b] = hist[q];
+  } else if (mode == kRefSort) {
+    const RefOut ro{K, row_slot, slot_row};
+    if (w < nwr)
+      group_rank(wk, w, lane, nkeys, nbits, cnt, [&](int64_t t, int key, int rank) { ro(t, (int64_t)kb[key] + rank); },
+                 [](int64_t) {});
+    if (b == 0) {
+      const int64_t chunk = max((int64_t)1, M / E);  // E equal chunks; rows past E*chunk are never computed
+      for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = (int)min((int64_t)e * chunk, M);
+    }
+  } else {
+    if (w < nwr)
+      group_rank(wk, w, lane, nkeys, nbits, cnt,
+                 [&](int64_t i, int key, int rank) {
+                   const int row = kb[key] + rank;
+                   row_slot[row] = (int)i;
+                   slot_row[i] = row;
+                 },
+                 [&](int64_t i) { slot_row[i] = -1; });
+    if (b == 0)
+      for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = kb[e];  // block 0: kb = key offsets
+    for (int64_t r = kb[E] + (int64_t)b * kPlanNT + threadIdx.x; r < M; r += (int64_t)nblk * kPlanNT)
+      row_slot[r] = -1;  // no row past the kept ones
   }
 }
 
@@ -176,34 +474,44 @@ __global__ void k_fill_i32(int* __restrict__ p, int n, int v) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
 }
 
-// Reference layout: E equal chunks of chunk = max(1, R / E) rows (rows past E*chunk are never computed).
-__global__ void k_plan_ref_offsets(int64_t R, int E, int* __restrict__ offsets) {
-  const int64_t chunk = max((int64_t)1, R / E);
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = (int)min((int64_t)e * chunk, R);
-}
-
-// Routed layout: rows of dropped slots do not exist; pad row_slot with -1 past the kept rows.
-__global__ void k_plan_pad_rows(const int* __restrict__ offsets, int E, int64_t R, int* __restrict__ row_slot) {
-  const int64_t kept = offsets[E];
-  for (int64_t r = kept + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < R; r += (int64_t)gridDim.x * blockDim.x)
-    row_slot[r] = -1;
-}
-
 // ---------------------------------------------------------------------------
-// Permute: xp[r, :] = x[row_slot[r] / K, :] for r < offsets[E].  Byte copy in
-// 16-byte units (row_bytes % 16 == 0), one wave per row.
+// Permute: xp[slot_row[t*K+k], :] = x[t, :] for every slot with a computed row (0 <= row < offsets[E]).
+// One wave per token: the row is read once, in segments of up to 64 * NCH 16-byte chunks held in registers,
+// and written to each of the token's rows (rows of one token lie in different expert segments, so a
+// gather by row would read the token K times).  Streaming (non-temporal) stores; the rows are written once.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_permute(const uint8_t* __restrict__ x, const int* __restrict__ row_slot,
-                                                 const int* __restrict__ offsets, int E, int K, int64_t row_bytes,
-                                                 int64_t R, uint8_t* __restrict__ xp) {
+template <int NCH>
+__global__ __launch_bounds__(256) void k_permute(const uint8_t* __restrict__ x, const int* __restrict__ slot_row,
+                                                 const int* __restrict__ offsets, int E, int K, int64_t N,
+                                                 int64_t row_bytes, uint8_t* __restrict__ xp) {
   const int lane = threadIdx.x & 63;
-  const int64_t rows = min(R, (int64_t)offsets[E]);
+  const int live = offsets[E];
   const int64_t nv = row_bytes / 16;
-  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * 4) {
-    const int64_t t = row_slot[r] / K;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); t < N;
+       t += (int64_t)gridDim.x * 4) {
     const u32x4* src = reinterpret_cast<const u32x4*>(x + t * row_bytes);
-    u32x4* dst = reinterpret_cast<u32x4*>(xp + r * row_bytes);
-    for (int64_t v = lane; v < nv; v += 64) __builtin_nontemporal_store(src[v], dst + v);
+    for (int64_t c0 = 0; c0 < nv; c0 += 64 * NCH) {
+      u32x4 v[NCH];
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int64_t c = c0 + lane + 64 * j;
+        v[j] = c < nv ? __builtin_nontemporal_load(src + c) : u32x4{0u, 0u, 0u, 0u};
+      }
+      for (int kw = 0; kw < K; kw += 64) {
+        const int kn = min(K - kw, 64);
+        const int mine = lane < kn ? slot_row[t * K + kw + lane] : -1;
+        for (int k = 0; k < kn; ++k) {
+          const int r = __builtin_amdgcn_readlane(mine, k);
+          if (r < 0 || r >= live) continue;
+          u32x4* dst = reinterpret_cast<u32x4*>(xp + (int64_t)r * row_bytes);
+#pragma unroll
+          for (int j = 0; j < NCH; ++j) {
+            const int64_t c = c0 + lane + 64 * j;
+            if (c < nv) __builtin_nontemporal_store(v[j], dst + c);
+          }
+        }
+      }
+    }
   }
 }
 
@@ -511,9 +819,10 @@ size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct PlanWs {
   int nblk_max, nkeys_max;
-  size_t off_counts, off_base, off_totals, off_keyoff, total;
+  size_t off_counts, off_base, off_keytot, total;
 };
 
+// Block tables of the multi-block path (plans the single-block planner does not take; those need none).
 PlanWs plan_ws(int64_t N, int64_t K, int64_t E) {
   PlanWs p{};
   const int64_t M = std::max<int64_t>(1, N * K);
@@ -524,38 +833,57 @@ PlanWs plan_ws(int64_t N, int64_t K, int64_t E) {
   off += al256((size_t)p.nblk_max * p.nkeys_max * 4);
   p.off_base = off;
   off += al256((size_t)p.nblk_max * p.nkeys_max * 4);
-  p.off_totals = off;
-  off += al256((size_t)p.nkeys_max * 4);
-  p.off_keyoff = off;
+  p.off_keytot = off;
   off += al256((size_t)(p.nkeys_max + 1) * 4);
   p.total = off;
   return p;
 }
 
-int nbits_for(int nkeys) {
-  int b = 0;
-  while ((1 << b) < nkeys) ++b;
-  return b;
+// Dynamic LDS above the default 64 KB needs the kernel's attribute raised (once per kernel and size; every
+// device the library runs on gets the same value, so the largest size set so far covers the call).
+template <typename Kern>
+int plan_allow_lds(Kern kernel, size_t bytes, std::atomic<size_t>& set_so_far) {
+  if (bytes <= 64 * 1024 || bytes <= set_so_far.load()) return 0;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)bytes) != hipSuccess)
+    return check_launch("moe_plan: hipFuncSetAttribute");
+  size_t cur = set_so_far.load();
+  while (cur < bytes && !set_so_far.compare_exchange_weak(cur, bytes)) {
+  }
+  return 0;
 }
+std::atomic<size_t> g_lds_small{0}, g_lds_rank{0};
 
-int grouping(hipStream_t s, int mode, const int64_t* idx, uint8_t* drop, int64_t M, int K, int E, int nkeys,
-             int64_t capacity, const PlanWs& p, char* ws, int* key_off_out, int* row_slot, int* slot_row,
-             int* ndrop) {
-  const int nblk = (int)((M + kPlanIB - 1) / kPlanIB);
-  int* counts = reinterpret_cast<int*>(ws + p.off_counts);
-  int* base = reinterpret_cast<int*>(ws + p.off_base);
-  int* totals = reinterpret_cast<int*>(ws + p.off_totals);
-  int* key_off = key_off_out ? key_off_out : reinterpret_cast<int*>(ws + p.off_keyoff);
-  const size_t lds = (size_t)nkeys * 4;
-  MOE_LAUNCH("k_plan_count", k_plan_count, dim3(nblk), dim3(256), lds, s, mode, idx, drop, M, K, E, nkeys, counts,
-             ndrop);
-  MOE_LAUNCH("k_plan_scan_blocks", k_plan_scan_blocks, dim3((nkeys + 15) / 16), dim3(256), 0, s, counts, nblk, nkeys,
-             base, totals);
-  MOE_LAUNCH("k_plan_scan_keys", k_plan_scan_keys, dim3(1), dim3(1024), 0, s, totals, nkeys, key_off);
-  MOE_LAUNCH("k_plan_rank", k_plan_rank, dim3(nblk), dim3(64), lds, s, mode, idx, drop, M, K, E, nkeys,
-             nbits_for(nkeys), base, key_off, capacity, row_slot, slot_row, ndrop);
-  return check_launch("moe_plan grouping");
-}
+// The grouping passes of the multi-block path.  `counted`: the counts table already holds this grouping's
+// block counts (written by the capacity rank pass before it).
+struct Grouping {
+  hipStream_t s;
+  const PlanKeys& pk;
+  int64_t M;
+  const PlanWs& p;
+  char* ws;
+  uint8_t* drop;
+  int *row_slot, *slot_row, *offsets, *ndrop;
+
+  int run(int mode, int64_t nitems, int nkeys, int64_t capacity, bool zero_ndrop, bool counted,
+          bool emit_next) const {
+    const int nblk = (int)((nitems + kPlanIB - 1) / kPlanIB);
+    int* counts = reinterpret_cast<int*>(ws + p.off_counts);
+    int* base = reinterpret_cast<int*>(ws + p.off_base);
+    int* key_tot = reinterpret_cast<int*>(ws + p.off_keytot);
+    if (!counted)
+      MOE_LAUNCH("k_plan_count", k_plan_count, dim3(nblk), dim3(kPlanCountNT), (size_t)nkeys * 4, s, mode, pk,
+                 nitems, nkeys, nblk, counts, ndrop, zero_ndrop ? 1 : 0);
+    MOE_LAUNCH("k_plan_scan", k_plan_scan, dim3((nkeys + 3) / 4), dim3(256), 0, s, counts, nblk, nkeys, base,
+               key_tot);
+    const size_t lds_rank = (size_t)(plan_nwr(nkeys) * nkeys + nkeys + 1 + kPlanNT + 16 + pk.E) * 4;
+    if (int rc = plan_allow_lds(k_plan_rank, lds_rank, g_lds_rank)) return rc;
+    // the rank pass of the capacity grouping writes the next grouping's counts over its own (already scanned)
+    MOE_LAUNCH("k_plan_rank", k_plan_rank, dim3(nblk), dim3(kPlanNT), lds_rank, s, mode, pk, nitems, M, nkeys, nblk,
+               base, key_tot, capacity, drop, row_slot, slot_row, offsets, ndrop, emit_next ? counts : nullptr);
+    return check_launch("moe_plan grouping");
+  }
+};
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -581,33 +909,32 @@ int plan_check(int64_t N, int64_t K, int64_t E, int layout, const int32_t* offse
   return 0;
 }
 
-// The plan proper, with its block tables in `ws` (plan_ws(N, K, E).total bytes; every table is written
-// before it is read, so ws needs no initialisation).
+// The plan proper.  Small plans (plan_small_ok): one block does everything in LDS.  Beyond: count / scan /
+// rank kernels per grouping with their block tables in `ws` (plan_ws(N, K, E).total bytes; every table is
+// written before it is read, so ws needs no initialisation).
 int plan_run(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capacity, int layout, uint8_t* drop_out,
              int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop, char* ws, hipStream_t s) {
   const int64_t M = N * K;
-  const PlanWs p = plan_ws(N, K, E);
   uint8_t* drop = capacity >= 0 ? drop_out : nullptr;
+  const PlanKeys pk{idx, drop, (int)K, (int)E};
+  const int nk_max = drop ? (int)(K * E) : (int)E;
+  if (plan_small_ok(M, nk_max, (int)E)) {
+    const size_t lds = (size_t)(plan_small_cnt(nk_max, (int)E) + 2 * nk_max + 1 + kPlanNT + 16) * 4;
+    if (int rc = plan_allow_lds(k_plan_small, lds, g_lds_small)) return rc;
+    MOE_LAUNCH("k_plan_small", k_plan_small, dim3(1), dim3(kPlanNT), lds, s, idx, (int)N, (int)K, (int)E, capacity,
+               layout, drop, row_slot, slot_row, offsets, ndrop);
+    return check_launch("moe_plan");
+  }
+  const PlanWs p = plan_ws(N, K, E);
+  const Grouping g{s, pk, M, p, ws, drop, row_slot, slot_row, offsets, ndrop};
   if (drop) {
-    if (int rc = grouping(s, kCapacity, idx, drop, M, (int)K, (int)E, (int)(K * E), capacity, p, ws, nullptr,
-                          row_slot, slot_row, ndrop))
-      return rc;
-  } else {
-    MOE_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, s, ndrop, 1, 0);
+    // capacity drops; for the routed layout the same pass counts the kept slots per expert and block
+    if (int rc = g.run(kCapacity, M, (int)(K * E), capacity, true, false, layout == 1)) return rc;
+    if (layout == 0) return g.run(kRefSort, N, (int)E, -1, false, false, false);
+    return g.run(kRouted, M, (int)E, -1, false, true, false);
   }
-  if (layout == 0) {
-    if (int rc = grouping(s, kRefSort, idx, nullptr, N, (int)K, (int)E, (int)E, -1, p, ws, nullptr, row_slot,
-                          slot_row, ndrop))
-      return rc;
-    MOE_LAUNCH("k_plan_ref_offsets", k_plan_ref_offsets, dim3(1), dim3(256), 0, s, M, (int)E, offsets);
-  } else {
-    if (int rc = grouping(s, kRouted, idx, drop, M, (int)K, (int)E, (int)E, -1, p, ws, offsets, row_slot, slot_row,
-                          ndrop))
-      return rc;
-    MOE_LAUNCH("k_plan_pad_rows", k_plan_pad_rows, dim3((unsigned)std::min<int64_t>(1024, (M + 255) / 256)),
-               dim3(256), 0, s, offsets, (int)E, M, row_slot);
-  }
-  return check_launch("moe_plan");
+  if (layout == 0) return g.run(kRefSort, N, (int)E, -1, true, false, false);
+  return g.run(kRouted, M, (int)E, -1, true, false, false);
 }
 
 // An empty plan (N * K == 0): zero offsets and drop count.
@@ -687,17 +1014,24 @@ extern "C" int moe_plan_noalloc(const int64_t* idx, int64_t N, int64_t K, int64_
                   static_cast<char*>(ptr), s);
 }
 
-extern "C" int moe_permute(const void* x, int64_t row_bytes, const int32_t* row_slot, const int32_t* offsets,
-                           int64_t E, int64_t K, int64_t R, void* xp, void* stream) {
-  if (row_bytes <= 0 || row_bytes % 16 || E < 1 || K < 1 || R < 0)
+extern "C" int moe_permute(const void* x, int64_t row_bytes, const int32_t* slot_row, const int32_t* offsets,
+                           int64_t N, int64_t K, int64_t E, void* xp, void* stream) {
+  if (row_bytes <= 0 || row_bytes % 16 || E < 1 || K < 1 || N < 0)
     return fail_arg("moe_permute: bad arguments (row_bytes must be a positive multiple of 16)");
-  if (R == 0) return 0;
-  if (!x || !row_slot || !offsets || !xp || !al16(x) || !al16(xp))
+  if (N == 0) return 0;
+  if (!x || !slot_row || !offsets || !xp || !al16(x) || !al16(xp))
     return fail_arg("moe_permute: null or misaligned pointer");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const unsigned nb = (unsigned)std::min<int64_t>(8192, (R + 3) / 4);
-  MOE_LAUNCH("k_permute", k_permute, dim3(nb), dim3(256), 0, s, static_cast<const uint8_t*>(x), row_slot, offsets,
-             (int)E, (int)K, row_bytes, R, static_cast<uint8_t*>(xp));
+  const unsigned nb = (unsigned)std::min<int64_t>(8192, (N + 3) / 4);
+  const uint8_t* xb = static_cast<const uint8_t*>(x);
+  uint8_t* xpb = static_cast<uint8_t*>(xp);
+  // chunks a lane keeps: the whole row in one segment up to 8 KB (H = 4096 in bf16), 8 KB segments beyond
+  if (row_bytes <= 4 * 1024)
+    MOE_LAUNCH("k_permute", k_permute<4>, dim3(nb), dim3(256), 0, s, xb, slot_row, offsets, (int)E, (int)K, N,
+               row_bytes, xpb);
+  else
+    MOE_LAUNCH("k_permute", k_permute<8>, dim3(nb), dim3(256), 0, s, xb, slot_row, offsets, (int)E, (int)K, N,
+               row_bytes, xpb);
   return check_launch("moe_permute");
 }
 

@@ -6,9 +6,9 @@
 // would overflow fp32 (it does below 448 / FLT_MAX ~ 1.3e-36), turning 0 * inv into NaN -- is treated as a
 // zero row: scale 1, inv 1 (its elements, all below 2^-118, round to +-0).
 //
-// k_permute_fp8     the dispatch payload: row r of the permuted buffer is the quantized row of token
-//                   row_slot[r] / K (the rows k_permute copies), written at one byte per element -- half
-//                   the bytes of the bf16 permute -- with its scale in sx[r].
+// k_permute_fp8     the dispatch payload: each token row is quantized once and written to the rows of its
+//                   slots (the rows k_permute fills) at one byte per element -- half the bytes of the bf16
+//                   permute -- with its scale in sx[row].
 // k_quant_rows_fp8  any [rows, cols] matrix (the expert weights once, the SwiGLU activations per forward).
 //
 // One wave per row: pass 1 takes the row's absmax, pass 2 quantizes 8 elements per lane and stores them as
@@ -145,15 +145,46 @@ __global__ __launch_bounds__(256) void k_quant_rows_fp8(const T* __restrict__ sr
     quant_row<T>(src + r * ld, cols, dst + r * cols, scale + r, lane);
 }
 
+// The quantized dispatch payload, one wave per token: the token row is quantized once (absmax pass, then a
+// conversion pass) and each 8-byte word goes to every row the token's slots hold (rows in [0, offsets[E])),
+// with the row's scale.
 template <typename T>
-__global__ __launch_bounds__(256) void k_permute_fp8(const T* __restrict__ x, const int* __restrict__ row_slot,
-                                                    const int* __restrict__ offsets, int E, int K, int H, int64_t R,
+__global__ __launch_bounds__(256) void k_permute_fp8(const T* __restrict__ x, const int* __restrict__ slot_row,
+                                                    const int* __restrict__ offsets, int E, int K, int H, int64_t N,
                                                     uint8_t* __restrict__ xq, float* __restrict__ sx) {
   const int lane = threadIdx.x & 63;
-  const int64_t rows = min(R, (int64_t)offsets[E]);
-  for (int64_t r = (int64_t)blockIdx.x * 4 + q_wave(); r < rows; r += (int64_t)gridDim.x * 4) {
-    const int64_t t = __builtin_amdgcn_readfirstlane(row_slot[r]) / K;
-    quant_row<T>(x + t * H, H, xq + r * H, sx + r, lane);
+  const int live = offsets[E];
+  for (int64_t t = (int64_t)blockIdx.x * 4 + q_wave(); t < N; t += (int64_t)gridDim.x * 4) {
+    const T* src = x + t * H;
+    float amax = 0.f;
+    for (int c = lane * 8; c < H; c += 512) {
+      float v[8];
+      q_load8<T>(src + c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    }
+    amax = wave_max(amax);
+    float sc, inv;
+    row_scale(amax, sc, inv);
+    for (int kw = 0; kw < K; kw += 64) {
+      const int kn = min(K - kw, 64);
+      const int mine = lane < kn ? slot_row[t * K + kw + lane] : -1;
+      if (lane < kn && mine >= 0 && mine < live) sx[mine] = sc;
+      for (int c = lane * 8; c < H; c += 512) {
+        float v[8];
+        q_load8<T>(src + c, v);
+        uint32_t lo = 0, hi = 0;
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv, v[1] * inv, lo, false);
+        lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv, v[3] * inv, lo, true);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4] * inv, v[5] * inv, hi, false);
+        hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6] * inv, v[7] * inv, hi, true);
+        for (int k = 0; k < kn; ++k) {
+          const int r = __builtin_amdgcn_readlane(mine, k);
+          if (r >= 0 && r < live)
+            __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(xq + (int64_t)r * H + c));
+        }
+      }
+    }
   }
 }
 
@@ -200,20 +231,20 @@ extern "C" int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, 
   return quant_rows_fp8(src, src_dtype, rows, cols, ld, dst, scale, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int moe_permute_fp8(const void* x, int x_dtype, const int32_t* row_slot, const int32_t* offsets, int64_t E,
-                               int64_t K, int64_t H, int64_t R, void* xq, float* sx, void* stream) {
-  if (E < 1 || K < 1 || R < 0 || H < 16 || H % 16 || H > INT32_MAX / 2 || (x_dtype != MOE_BF16 && x_dtype != MOE_F32))
+extern "C" int moe_permute_fp8(const void* x, int x_dtype, const int32_t* slot_row, const int32_t* offsets, int64_t N,
+                               int64_t K, int64_t E, int64_t H, void* xq, float* sx, void* stream) {
+  if (E < 1 || K < 1 || N < 0 || H < 16 || H % 16 || H > INT32_MAX / 2 || (x_dtype != MOE_BF16 && x_dtype != MOE_F32))
     return fail_arg("moe_permute_fp8: bad arguments (need H %% 16 == 0, bf16 or fp32 x)");
-  if (R == 0) return 0;
-  if (!x || !row_slot || !offsets || !xq || !sx || !al16q(x) || !al16q(xq))
+  if (N == 0) return 0;
+  if (!x || !slot_row || !offsets || !xq || !sx || !al16q(x) || !al16q(xq))
     return fail_arg("moe_permute_fp8: null or misaligned pointer");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (x_dtype == MOE_BF16)
-    MOE_LAUNCH("k_permute_fp8", k_permute_fp8<uint16_t>, dim3(q_blocks(R)), dim3(256), 0, s,
-               static_cast<const uint16_t*>(x), row_slot, offsets, (int)E, (int)K, (int)H, R,
+    MOE_LAUNCH("k_permute_fp8", k_permute_fp8<uint16_t>, dim3(q_blocks(N)), dim3(256), 0, s,
+               static_cast<const uint16_t*>(x), slot_row, offsets, (int)E, (int)K, (int)H, N,
                static_cast<uint8_t*>(xq), sx);
   else
-    MOE_LAUNCH("k_permute_fp8", k_permute_fp8<float>, dim3(q_blocks(R)), dim3(256), 0, s, static_cast<const float*>(x),
-               row_slot, offsets, (int)E, (int)K, (int)H, R, static_cast<uint8_t*>(xq), sx);
+    MOE_LAUNCH("k_permute_fp8", k_permute_fp8<float>, dim3(q_blocks(N)), dim3(256), 0, s, static_cast<const float*>(x),
+               slot_row, offsets, (int)E, (int)K, (int)H, N, static_cast<uint8_t*>(xq), sx);
   return check_launch("moe_permute_fp8");
 }

@@ -343,15 +343,16 @@ def plan(idx: torch.Tensor, num_experts: int, capacity: int = -1, layout: int = 
 
 
 def permute(x: torch.Tensor, p: Plan) -> torch.Tensor:
-    """xp [N*K, H]: row r holds x[row_slot[r] // K] (rows past offsets[E] are left unwritten)."""
+    """xp [N*K, H]: row slot_row[t*K+k] holds x[t] (one read of each token row; rows past offsets[E] are left
+    unwritten)."""
     dev = L.require_device(x)
     x = x.contiguous()
     H = x.shape[1]
     xp = torch.empty((p.rows, H), dtype=x.dtype, device=dev)
     if p.rows == 0:
         return xp
-    rc = L.load().moe_permute(x.data_ptr(), H * x.element_size(), p.row_slot.data_ptr(), p.offsets.data_ptr(),
-                              p.E, p.K, p.rows, xp.data_ptr(), L.stream_of(dev))
+    rc = L.load().moe_permute(x.data_ptr(), H * x.element_size(), p.slot_row.data_ptr(), p.offsets.data_ptr(),
+                              p.N, p.K, p.E, xp.data_ptr(), L.stream_of(dev))
     L.check(rc, "moe_permute")
     return xp
 
@@ -457,8 +458,8 @@ def permute_fp8(x: torch.Tensor, p: Plan) -> Tuple[torch.Tensor, torch.Tensor]:
     sx = torch.empty((p.rows,), dtype=torch.float32, device=dev)
     if p.rows == 0:
         return xq, sx
-    rc = L.load().moe_permute_fp8(x.data_ptr(), L.dtype_code(x.dtype), p.row_slot.data_ptr(), p.offsets.data_ptr(),
-                                  p.E, p.K, H, p.rows, xq.data_ptr(), sx.data_ptr(), L.stream_of(dev))
+    rc = L.load().moe_permute_fp8(x.data_ptr(), L.dtype_code(x.dtype), p.slot_row.data_ptr(), p.offsets.data_ptr(),
+                                  p.N, p.K, p.E, H, xq.data_ptr(), sx.data_ptr(), L.stream_of(dev))
     L.check(rc, "moe_permute_fp8")
     return xq, sx
 

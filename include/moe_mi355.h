@@ -172,11 +172,12 @@ int moe_plan_noalloc(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_
                      uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
                      void* stream);
 
-/* Permute (dispatch): xp[r] = x[row_slot[r] / K] for r < offsets[E]; rows are
- * row_bytes long (a multiple of 16).  Replaces flat[sort_order]
- * .repeat_interleave(K) (pkg/distributed/moe_layer.py L:318-319). */
-int moe_permute(const void* x, int64_t row_bytes, const int32_t* row_slot, const int32_t* offsets,
-                int64_t E, int64_t K, int64_t R, void* xp, void* stream);
+/* Permute (dispatch): xp[slot_row[t*K+k]] = x[t] for every slot whose row is computed (0 <= row <
+ * offsets[E]); other rows of xp are left unwritten.  Rows are row_bytes long (a multiple of 16); each token
+ * row is read once and written to its K rows.  Replaces flat[sort_order].repeat_interleave(K)
+ * (pkg/distributed/moe_layer.py L:318-319). */
+int moe_permute(const void* x, int64_t row_bytes, const int32_t* slot_row, const int32_t* offsets,
+                int64_t N, int64_t K, int64_t E, void* xp, void* stream);
 
 /* Weighted combine: out[t] = sum_k w[t,k] y[slot_row[t*K+k]] over slots that
  * have a computed row and are not dropped (drop may be NULL); fp32 sums, one
@@ -234,9 +235,9 @@ int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* 
  *
  * moe_quant_rows_fp8: src [rows, ld] (MOE_BF16 / MOE_F32, first `cols`
  * columns) -> dst [rows, cols] e4m3 bytes, scale [rows] f32.  cols % 16 == 0.
- * moe_permute_fp8: the quantized dispatch payload: row r of xq [R, H] is
- * token row_slot[r] / K of x quantized, sx [R] its scale (rows the plan
- * leaves empty are not written).
+ * moe_permute_fp8: the quantized dispatch payload: row slot_row[t*K+k] of
+ * xq [N*K, H] is token t of x quantized, sx its scale (rows the plan leaves
+ * empty, or past offsets[E], are not written).
  * moe_swiglu_fwd_fp8: act, hgu, y as moe_swiglu_fwd (bf16) from xq / sx and
  * the quantized weights wg_q, wu_q [E, F, H], wd_q [E, H, F] with scales
  * sg, su [E, F], sd [E, H] (moe_quant_rows_fp8 over the weight rows); act
@@ -245,8 +246,8 @@ int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* 
  * ---------------------------------------------------------------------- */
 int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst,
                        float* scale, void* stream);
-int moe_permute_fp8(const void* x, int x_dtype, const int32_t* row_slot, const int32_t* offsets, int64_t E,
-                    int64_t K, int64_t H, int64_t R, void* xq, float* sx, void* stream);
+int moe_permute_fp8(const void* x, int x_dtype, const int32_t* slot_row, const int32_t* offsets, int64_t N,
+                    int64_t K, int64_t E, int64_t H, void* xq, float* sx, void* stream);
 size_t moe_swiglu_fwd_fp8_workspace(int64_t R, int64_t F, int64_t E);
 int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* wg_q, const float* sg, const void* wu_q,
                        const float* su, const void* wd_q, const float* sd, const int32_t* offsets, int64_t R,

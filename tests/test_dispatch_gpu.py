@@ -36,6 +36,11 @@ CASES = [
     (16, 1, 1, None, 0.0),
     (8, 8, 8, 1.0, 0.0),
     (65536, 6, 64, 1.25, 0.0),  # C3 shape
+    (2048, 8, 64, 1.0, 1.0),  # 16384 slots: the largest single-block plan
+    (16385, 1, 4, 1.0, 0.0),  # one slot more: the multi-block planner
+    (16384, 1, 1024, None, 0.0),  # single block, 1024 keys
+    (1500, 8, 1024, 1.0, 2.0),  # 8192 capacity keys: too many for one block's waves at 12000 slots
+    (3000, 8, 1024, 1.25, 0.0),  # the same keys over several blocks
 ]
 
 
