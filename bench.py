@@ -6,15 +6,20 @@
 Workloads (inputs drawn on the CPU from fixed seeds, resident in HBM before
 timing starts; ``moe_mi355/configs.py``):
 
-  layer   C4 (headline): full MoE layer fwd+bwd, T=8192 d=4096 E=8 SwiGLU
-          F=14336 K=2, bf16 -- router, planner, permute, grouped gate/up/down
-          GEMM, combine, and the whole backward.  ``value`` = tokens/s.
-  router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2 (measured with the
-          layer too, reported under "router").
+  layer   (default) C4, the headline line: full MoE layer fwd+bwd, T=8192
+          d=4096 E=8 SwiGLU F=14336 K=2, bf16 -- router, planner, permute,
+          grouped gate/up/down GEMM, combine, and the whole backward.
+          ``value`` = tokens/s.  The same run measures every other config
+          under its own key: "router" (C2), "c1", "norm_router", "fp8_fwd",
+          "dispatch" (C3) and "skewed" (C5), each with its roofline and,
+          where the config has one, its CPU baseline.
+  router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2.
+  c1      C1: router fwd+bwd, T=4096 d=512 E=8 K=2, fp32, aux 0.01 + z 1e-3,
+          timed the reference's way (3 warmup + 20 timed, mean +- std), beside
+          the float64 oracle of the same step on the CPU.
   norm_router  C2 shape with the block's RMSNorm in front of the router:
           the norm fused into the router's read of the hidden state, fwd+bwd,
-          beside the unfused composition and a torch-ops norm (measured with
-          the layer too, under "norm_router").
+          beside the unfused composition and a torch-ops norm.
   dispatch C3: router + planner + permute + combine forward, T=65536 d=2048
           E=64 K=6, cf=1.25 with drops.
   skewed  C5: layer fwd+bwd, T=32768 d=2048 E=128 F=768 K=8, cf=1.0 drops,
@@ -28,8 +33,11 @@ prints ONE JSON line on stdout.  Per-kernel durations come from a separate
 pass (after the timed one) in which libmoe_mi355.so records hipEvents around
 each of its launches on the launch stream.  The router leg is also replayed
 as a captured HIP graph (``graph_*`` fields: the rate without host launch
-overhead).  The CPU baseline is the float64 oracle
-timed on a bounded sample of the same workload on this host's cores.
+overhead).  The CPU baselines are the float64 oracle timed on a bounded
+sample of the same workload (the whole config for C1) on this host's cores.
+The headline layer is timed with check_numerics=False; the layer's default
+configuration (per-forward NaN assert and checked router statistics, each
+with a host synchronisation) is timed too ("check_numerics_ms_per_step").
 """
 
 from __future__ import annotations
@@ -115,6 +123,24 @@ def timed(torch, step, steps, warmup, prof_steps=None):
     torch.cuda.synchronize()
     _lib.prof_enable(False)
     return ms, _lib.prof_summary()
+
+
+def mean_std_ms(fn, warmup=3, iters=20, sync=None):
+    """The reference's timing (run_benchmark.py L:63-79): ``warmup`` untimed calls, then ``iters`` calls each
+    timed on the host clock (after a device synchronize when ``sync`` is given); mean and population std."""
+    for _ in range(warmup):
+        fn()
+    if sync:
+        sync()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        if sync:
+            sync()
+        times.append((time.perf_counter() - t0) * 1e3)
+    mean = sum(times) / len(times)
+    return mean, (sum((t - mean) ** 2 for t in times) / len(times)) ** 0.5
 
 
 def graph_timed(torch, step, steps, warmup):
@@ -229,6 +255,50 @@ def cpu_baseline_router(torch, budget_s=12.0):
 
 
 # ---------------------------------------------------------------------------
+# C1: the reference's CPU-runnable router config (fp32, aux and z losses)
+# ---------------------------------------------------------------------------
+def run_c1(args, torch, with_cpu=True):
+    """Router fwd+bwd at C1 (T=4096, d=512, E=8, K=2, fp32, seed 0, aux 0.01, z 1e-3) on the GPU and, as the
+    CPU baseline, the float64 oracle of the same step (oracle/router.py router_full), both timed the
+    reference's way: 3 warmup + 20 timed calls, mean +- std (run_benchmark.py L:63-79)."""
+    from moe_mi355 import configs
+    from moe_mi355.router import RouterCore
+
+    cfg = configs.C1
+    inp = configs.router_inputs(cfg)
+    dev = torch.device("cuda:0")
+    x = inp["x"].to(dev).requires_grad_(True)
+    w = inp["gate_w"].to(dev).requires_grad_(True)
+    gw = inp["grad_w"].to(dev)
+    one = torch.ones((), device=dev)
+    N, H, E, K = cfg.T, cfg.H, cfg.E, cfg.K
+
+    def step():
+        out = RouterCore.apply(x, w, K, cfg.aux_coef, cfg.z_coef, None)
+        torch.autograd.grad([out[1], out[2], out[3]], (x, w), grad_outputs=[gw, one, one])
+
+    mean, std = mean_std_ms(step, sync=torch.cuda.synchronize)
+    ms, _ = timed(torch, step, max(args.steps, 20), args.warmup, prof_steps=1)
+    nbytes = 3 * N * H * 4 + 2 * H * E * 4 + 2 * N * E * 4 + N * K * (8 + 4 + 4) + E * 8
+    res = {"workload": "C1 router fwd+bwd, fp32, aux 0.01 + z 1e-3", "tokens": N, "d_model": H, "experts": E,
+           "top_k": K, "ms_mean": round(mean, 4), "ms_std": round(std, 4), "tokens_per_s": N / (mean * 1e-3),
+           "pipelined_ms_per_step": ms, "pipelined_tokens_per_s": N / (ms * 1e-3),
+           "fwd_bwd_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    if with_cpu:
+        from oracle import router as OR
+
+        xc, wc, gc = inp["x"], inp["gate_w"], inp["grad_w"]
+        cm, cs = mean_std_ms(lambda: OR.router_full(xc, wc, K, grad_w=gc, alpha=cfg.aux_coef, beta=cfg.z_coef))
+        res["cpu_baseline"] = {
+            "value": N / (cm * 1e-3), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "ms_mean": round(cm, 3), "ms_std": round(cs, 3),
+            "sample": "the whole C1 config: float64 oracle router fwd+bwd with aux and z losses (oracle/router.py "
+                      "router_full), T=4096 d=512 E=8 K=2, seed 0, 3 warmup + 20 timed calls"}
+        res["gpu_vs_cpu"] = round(cm / mean, 1)
+    return res
+
+
+# ---------------------------------------------------------------------------
 # layer (C4, C5)
 # ---------------------------------------------------------------------------
 GEMM_KERNELS = ("k_gemm_swiglu_fwd1", "k_gemm_swiglu_fwd2", "k_gemm_swiglu_dact", "k_gemm_swiglu_dxp",
@@ -240,6 +310,18 @@ def gemm_flops(R, H, F):
     return {"k_gemm_swiglu_fwd1": 2 * R * H * 2 * F, "k_gemm_swiglu_fwd2": 2 * R * F * H,
             "k_gemm_swiglu_dact": 2 * R * H * F, "k_gemm_swiglu_dxp": 2 * R * 2 * F * H,
             "k_gemm_swiglu_dwd": 2 * R * H * F, "k_gemm_swiglu_dw1": 2 * R * 2 * F * H}
+
+
+def layer_hbm_bytes(N, H, E, K, R):
+    """Algorithmic HBM bytes per launch of the layer's data-movement and router kernels (bf16 rows, R computed
+    rows): each token row is read once by the permute and written to its rows; the combine reads the rows and
+    writes the tokens; the backward passes mirror them."""
+    return {"k_permute": N * H * 2 + R * H * 2 + N * K * 4,
+            "k_combine": R * H * 2 + N * H * 2 + N * K * (2 + 4 + 1),
+            "k_combine_bwd": N * H * 2 + 2 * R * H * 2 + N * K * (2 + 4 + 1 + 2),
+            "k_unpermute_sum": R * H * 2 + N * H * 2 + N * K * 4,
+            "k_router_fwd_bf16": N * H * 2 + H * E * 2 + N * E * 4 + N * 4 + N * K * (8 + 2),
+            "k_router_dxdw_bf16": 2 * N * H * 2 + N * E * 2 + H * E * 2}
 
 
 def build_layer(cfg, torch, inp, layout):
@@ -260,7 +342,7 @@ def build_layer(cfg, torch, inp, layout):
     return layer
 
 
-def run_layer(args, torch, cfg, layout, inp):
+def run_layer(args, torch, cfg, layout, inp, default_numerics=False):
     dev = torch.device("cuda:0")
     layer = build_layer(cfg, torch, inp, layout)
     x = inp["x"].to(dev).requires_grad_(True)
@@ -280,8 +362,23 @@ def run_layer(args, torch, cfg, layout, inp):
     log(f"[bench] timing {cfg.name}")
     ms, prof = timed(torch, step, args.steps, args.warmup, prof_steps=min(args.steps, 5))
     R = int(layer.last_plan.offsets[-1].item())  # rows run through the experts
+    expert_ms = layer.last_expert_compute_ms
+    numerics_ms = None
+    if default_numerics:
+        # the layer's default configuration: the per-forward NaN assert and the router's checked statistics,
+        # each with its host synchronisation (the timed steps above run with check_numerics=False)
+        layer.check_numerics = True
+        layer.router.sync_profile = True
+        numerics_ms, _ = timed(torch, step, args.steps, args.warmup, prof_steps=1)
+        layer.check_numerics = False
+        layer.router.sync_profile = False
     fl = gemm_flops(R, cfg.H, cfg.F)
     kernels = kernel_table(prof, fl, 1e12, "TFLOPs")
+    hbm = layer_hbm_bytes(cfg.T, cfg.H, cfg.E, cfg.K, R)
+    for name, ent in kernel_table(prof, hbm, 1e9, "GBps").items():
+        if name in hbm:
+            kernels[name].update(ent)
+            kernels[name]["frac_of_hbm_peak"] = round(ent["GBps"] / HBM_PEAK_GBS, 4)
     dom = max((k for k in kernels if k in fl), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     achieved = kernels[dom]["TFLOPs"]
     step_flops = 18 * R * cfg.H * cfg.F
@@ -291,6 +388,8 @@ def run_layer(args, torch, cfg, layout, inp):
         "experts": cfg.E, "ffn": cfg.F, "top_k": cfg.K, "rows_computed": R,
         "capacity_factor": cfg.capacity_factor if cfg.capacity_dropping else None,
         "ms_per_step": ms, "tokens_per_s": cfg.T / (ms * 1e-3),
+        "check_numerics_ms_per_step": numerics_ms,
+        "last_expert_compute_ms": round(expert_ms, 4),
         "expert_TFLOP_per_step": step_flops / 1e12,
         "step_TFLOPs": round(step_flops / (ms * 1e-3) / 1e12, 2),
         "step_frac_of_mfma_peak": round(step_flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -359,26 +458,37 @@ def configs_mod():
     return configs
 
 
-def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=64, budget_s=15.0):
-    """float64 oracle layer fwd+bwd on the first ``sample_T`` tokens with the full-size weights."""
+def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=32, budget_s=12.0, min_reps=3):
+    """float64 oracle layer fwd+bwd on the first ``sample_T`` tokens with the full-size weights (converted to
+    float64 once, before timing), at least ``min_reps`` reps; mean +- std per rep."""
     from oracle import layer as OL
     from oracle import plan as OP
 
-    x = inp["x"][:sample_T]
-    g = inp["grad_out"][:sample_T]
+    f64 = {k: inp[k].double() for k in ("gate_w", "w_gate", "w_up", "w_down")}
+    x = inp["x"][:sample_T].double()
+    g = inp["grad_out"][:sample_T].double()
     lay = OP.LAYOUT_REFERENCE if layout == "reference" else OP.LAYOUT_ROUTED
-    n, t0 = 0, time.perf_counter()
-    while True:
-        OL.layer_fwd_bwd(x, inp["gate_w"], inp["w_gate"], inp["w_up"], inp["w_down"], cfg.K, grad_out=g,
+    bias = inp.get("bias")
+
+    def rep():
+        OL.layer_fwd_bwd(x, f64["gate_w"], f64["w_gate"], f64["w_up"], f64["w_down"], cfg.K, grad_out=g,
                          capacity_factor=cfg.capacity_factor, capacity_dropping=cfg.capacity_dropping, layout=lay,
-                         alpha=cfg.aux_coef, beta=cfg.z_coef, bias=inp.get("bias"))
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
-            break
-    return {"value": n * sample_T / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                         alpha=cfg.aux_coef, beta=cfg.z_coef, bias=bias)
+
+    rep()  # warmup
+    times, t0 = [], time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t0 < budget_s and len(times) < 50):
+        a = time.perf_counter()
+        rep()
+        times.append(time.perf_counter() - a)
+    mean = sum(times) / len(times)
+    std = (sum((t - mean) ** 2 for t in times) / len(times)) ** 0.5
+    del f64
+    return {"value": sample_T / mean, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "ms_mean": round(mean * 1e3, 1), "ms_std": round(std * 1e3, 1),
             "sample": f"float64 oracle layer fwd+bwd (oracle/layer.py layer_fwd_bwd) on the first {sample_T} "
-                      f"tokens of {cfg.name} with the full-size expert weights, {n} reps in {el:.1f} s"}
+                      f"tokens of {cfg.name} with the full-size expert weights (converted to float64 before "
+                      f"timing), {len(times)} reps after 1 warmup"}
 
 
 # ---------------------------------------------------------------------------
@@ -456,7 +566,7 @@ def run_norm_router(args, torch):
 # ---------------------------------------------------------------------------
 # dispatch (C3)
 # ---------------------------------------------------------------------------
-def run_dispatch(args, torch):
+def run_dispatch(args, torch, with_cpu=True):
     from moe_mi355 import configs, ops
 
     cfg = configs.C3
@@ -474,17 +584,73 @@ def run_dispatch(args, torch):
         state["out"] = ops.combine(xp, wt, p)
         state["p"] = p
 
+    log("[bench] timing C3")
     ms, prof = timed(torch, step, args.steps, args.warmup)
     R = int(state["p"].offsets[-1].item())
     N, H, E, K = cfg.T, cfg.H, cfg.E, cfg.K
-    work = {"k_router_fwd_bf16": N * H * 2 + H * E * 2 + N * E * 4 + N * 4 + N * K * 10,
-            "k_permute": 2 * R * H * 2 + R * 4,
-            "k_combine": R * H * 2 + N * H * 2 + N * K * (2 + 4 + 1)}
+    hbm = layer_hbm_bytes(N, H, E, K, R)
+    work = {k: hbm[k] for k in ("k_router_fwd_bf16", "k_permute", "k_combine")}
     kernels = kernel_table(prof, work, 1e9, "GBps")
+    for k in work:
+        if k in kernels:
+            kernels[k]["frac_of_hbm_peak"] = round(kernels[k]["GBps"] / HBM_PEAK_GBS, 4)
+    dom = max((k for k in kernels if k in work), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     total = sum(work.values())
-    return {"workload": "C3 router + plan + permute + combine (routed layout, cf=1.25 drops)", "tokens": N,
-            "rows_kept": R, "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3),
-            "GBps": round(total / (ms * 1e-3) / 1e9, 1), "kernels": kernels}
+    res = {"workload": "C3 router + plan + permute + combine (routed layout, cf=1.25 drops)", "tokens": N,
+           "d_model": H, "experts": E, "top_k": K, "rows_kept": R, "ms_per_step": ms,
+           "tokens_per_s": N / (ms * 1e-3), "alg_bytes_per_step": total,
+           "GBps": round(total / (ms * 1e-3) / 1e9, 1),
+           "roofline": {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["GBps"], "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(kernels[dom]["GBps"] / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic(dom, cfg.name), "alg_bytes_per_launch": work[dom],
+                        "avg_us": kernels[dom]["avg_us"]},
+           "kernels": kernels}
+    if with_cpu:
+        res["cpu_baseline"] = cpu_baseline_dispatch(torch, cfg, inp)
+    return res
+
+
+def cpu_baseline_dispatch(torch, cfg, inp, sample_T=8192, budget_s=6.0):
+    """The C3 step on the CPU for the first ``sample_T`` tokens: float64 oracle routing (oracle/router.py
+    route_fwd), the oracle's capacity drop mask and routed plan (oracle/plan.py), then the permute (gather of
+    token rows into expert order) and the weighted combine in float32 torch ops."""
+    from oracle import plan as OP
+    from oracle import router as OR
+
+    x = inp["x"][:sample_T]
+    gw = inp["gate_w"]
+    K, E = cfg.K, cfg.E
+    cap = OR.capacity_budget(sample_T, K, E, cfg.capacity_factor)
+
+    def rep():
+        f = OR.route_fwd(x, gw, K)
+        idx = f["idx"]
+        v = f["probs"].gather(1, idx)
+        wt = (v / v.sum(-1, keepdim=True)).float()
+        drop = OP.drop_mask(idx.numpy(), cap)
+        pl = OP.plan_routed(idx.numpy(), E, drop)
+        R = int(pl["n_rows"])
+        rs = torch.from_numpy(pl["row_slot"][:R].astype("int64"))
+        xp = x[rs // K].float()  # permute
+        sr = torch.from_numpy(pl["slot_row"].astype("int64")).view(-1, K)
+        out = torch.zeros(sample_T, x.shape[1])
+        for k in range(K):  # combine
+            keep = sr[:, k] >= 0
+            out[keep] += wt[keep, k:k + 1] * xp[sr[keep, k]]
+        return out
+
+    rep()
+    times, t0 = [], time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t0 < budget_s and len(times) < 50):
+        a = time.perf_counter()
+        rep()
+        times.append(time.perf_counter() - a)
+    mean = sum(times) / len(times)
+    std = (sum((t - mean) ** 2 for t in times) / len(times)) ** 0.5
+    return {"value": sample_T / mean, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "ms_mean": round(mean * 1e3, 1), "ms_std": round(std * 1e3, 1),
+            "sample": f"first {sample_T} tokens of C3: float64 oracle routing + oracle drop mask and routed plan "
+                      f"+ float32 torch permute and combine, {len(times)} reps after 1 warmup"}
 
 
 def add_mfma_ceiling(roof, extra, fp8):
@@ -507,7 +673,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="layer", choices=["layer", "router", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
+    ap.add_argument("--workload", default="layer", choices=["layer", "router", "c1", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
     ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -529,23 +695,38 @@ def main():
     if args.copy_probe:
         copy_probe(torch)
     extra = {}
+    with_cpu = not args.no_cpu_baseline
     if args.workload in ("layer", "all"):
+        # every config of the benchmark: C4 (the headline line), C2, C1, the fused norm, fp8, C3, C5
         log("[bench] generating C4 inputs")
         inp = configs.layer_inputs(configs.C4)
-        main_res = run_layer(args, torch, configs.C4, args.layout, inp)
+        main_res = run_layer(args, torch, configs.C4, args.layout, inp, default_numerics=True)
         log(f"[bench] layer: {main_res['ms_per_step']:.3f} ms/step")
         extra["router"] = run_router(args, torch)
         log(f"[bench] router: {extra['router']['ms_per_step']:.4f} ms/step")
+        extra["c1"] = run_c1(args, torch, with_cpu=with_cpu)
+        log(f"[bench] C1 router: {extra['c1']['ms_mean']:.4f} ms/step")
         extra["norm_router"] = run_norm_router(args, torch)
         log(f"[bench] norm_router: {extra['norm_router']['ms_per_step']:.4f} ms/step")
         extra["fp8_fwd"] = run_fp8_fwd(args, torch, inp)
         add_mfma_ceiling(extra["fp8_fwd"]["roofline"], extra["fp8_fwd"], fp8=True)
         log(f"[bench] fp8 forward: {extra['fp8_fwd']['fp8_ms_per_step']:.3f} ms/step "
             f"(bf16 forward {extra['fp8_fwd']['bf16_ms_per_step']:.3f})")
-        cpu = None if args.no_cpu_baseline else cpu_baseline_layer(torch, configs.C4, args.layout, inp)
+        log("[bench] CPU baselines (C4 layer sample, C2 router sample)")
+        cpu = cpu_baseline_layer(torch, configs.C4, args.layout, inp) if with_cpu else None
         del inp
-        if not args.no_cpu_baseline:
+        if with_cpu:
             extra["router"]["cpu_baseline"] = cpu_baseline_router(torch)
+        extra["dispatch"] = run_dispatch(args, torch, with_cpu=with_cpu)
+        log(f"[bench] C3 dispatch: {extra['dispatch']['ms_per_step']:.4f} ms/step")
+        log("[bench] generating C5 inputs")
+        inp5 = configs.layer_inputs(configs.C5)
+        extra["skewed"] = run_layer(args, torch, configs.C5, "routed", inp5)
+        log(f"[bench] C5 skewed layer: {extra['skewed']['ms_per_step']:.3f} ms/step")
+        if with_cpu:
+            extra["skewed"]["cpu_baseline"] = cpu_baseline_layer(torch, configs.C5, "routed", inp5, sample_T=64,
+                                                                 budget_s=6.0, min_reps=2)
+        del inp5
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
         add_mfma_ceiling(roof, extra, fp8=False)
@@ -571,21 +752,24 @@ def main():
         add_mfma_ceiling(roof, extra, fp8=True)
         config = {"workload": main_res.pop("workload"), "tokens": main_res.pop("tokens")}
     elif args.workload == "dispatch":
-        main_res = run_dispatch(args, torch)
-        cpu = None
+        main_res = run_dispatch(args, torch, with_cpu=with_cpu)
+        cpu = main_res.pop("cpu_baseline", None)
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "top_k")}
+    elif args.workload == "c1":
+        main_res = run_c1(args, torch, with_cpu=with_cpu)
+        cpu = main_res.pop("cpu_baseline", None)
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_mean"]
         roof = None
-        config = {"workload": main_res.pop("workload"), "tokens": main_res.pop("tokens")}
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "top_k")}
     else:
         inp = configs.layer_inputs(configs.C5)
         main_res = run_layer(args, torch, configs.C5, "routed", inp)
-        cpu = None if args.no_cpu_baseline else cpu_baseline_layer(torch, configs.C5, "routed", inp)
+        cpu = cpu_baseline_layer(torch, configs.C5, "routed", inp, sample_T=64) if with_cpu else None
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
-    if args.workload == "all":
-        extra["dispatch"] = run_dispatch(args, torch)
-        extra["skewed"] = run_layer(args, torch, configs.C5, "routed", configs.layer_inputs(configs.C5))
     main_res.pop("ms_per_step", None)
     main_res.pop("tokens_per_s", None)
     out = {

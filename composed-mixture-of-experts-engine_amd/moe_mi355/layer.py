@@ -17,10 +17,15 @@ from . import ops
 
 class ExpertsFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, w_gate, w_up, w_down, p: ops.Plan, keep_preact: bool = True):
+    def forward(ctx, x, w, w_gate, w_up, w_down, p: ops.Plan, keep_preact: bool = True, timer=None):
         xp = ops.permute(x, p)
+        # timer (optional): an object with start() / stop(), bracketing the expert GEMMs on the stream
+        if timer is not None:
+            timer.start()
         # keep_preact=False (the caller knows no backward follows) skips storing the pre-activations
         act, hgu, y = ops.swiglu_forward(xp, w_gate, w_up, w_down, p.offsets, keep_preact=keep_preact)
+        if timer is not None:
+            timer.stop()
         out = ops.combine(y, w, p)
         ctx.save_for_backward(w, w_gate, w_up, w_down, xp, act, hgu, y)
         ctx.p = p
@@ -33,7 +38,7 @@ class ExpertsFn(torch.autograd.Function):
         dy, dw = ops.combine_backward(dout, y, w, p, need_dw=ctx.needs_input_grad[1])
         dxp, dwg, dwu, dwd = ops.swiglu_backward(dy, xp, act, hgu, w_gate, w_up, w_down, p.offsets)
         dx = ops.unpermute_sum(dxp, p) if ctx.needs_input_grad[0] else None
-        return dx, dw, dwg, dwu, dwd, None, None
+        return dx, dw, dwg, dwu, dwd, None, None, None
 
 
 class PermuteFn(torch.autograd.Function):

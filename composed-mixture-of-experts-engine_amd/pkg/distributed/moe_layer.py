@@ -51,6 +51,32 @@ __all__ = ["DistributedMoELayer", "compute_capacity_drop_mask", "_cumcount"]
 _LAYOUTS = {"reference": ops.LAYOUT_REFERENCE, "routed": ops.LAYOUT_ROUTED}
 
 
+class _ExpertTimer:
+    """Two timing events on the current stream around the expert compute; the elapsed time is read only when
+    asked for.  None on the CPU and under graph capture."""
+
+    __slots__ = ("a", "b")
+
+    @classmethod
+    def new(cls, like: torch.Tensor) -> Optional["_ExpertTimer"]:
+        if not like.is_cuda or torch.cuda.is_current_stream_capturing():
+            return None
+        t = cls()
+        t.a = torch.cuda.Event(enable_timing=True)
+        t.b = torch.cuda.Event(enable_timing=True)
+        return t
+
+    def start(self) -> None:
+        self.a.record()
+
+    def stop(self) -> None:
+        self.b.record()
+
+    def elapsed_ms(self) -> float:
+        self.b.synchronize()
+        return max(float(self.a.elapsed_time(self.b)), 0.0)
+
+
 def _cumcount(groups: torch.Tensor) -> torch.Tensor:
     """Each element's 0-based position among earlier elements of its group (L:64-115).
 
@@ -164,7 +190,8 @@ class DistributedMoELayer(nn.Module):
             self.router.to(dev)
         self.last_dispatch_ms: float = 0.0
         self.last_combine_ms: float = 0.0
-        self.last_expert_compute_ms: float = 0.0
+        self._expert_ms: float = 0.0
+        self._expert_timer: Optional[_ExpertTimer] = None
         self.last_overlap_ratio: float = 0.0
         self.last_plan: Optional[ops.Plan] = None
         self._register_state_dict_hook(DistributedMoELayer._to_reference_keys)
@@ -188,6 +215,22 @@ class DistributedMoELayer(nn.Module):
             keys = [f"{prefix}experts.{i}.{name}.weight" for i in range(getattr(module, name).shape[0])]
             if all(k in state_dict for k in keys):
                 state_dict[prefix + name] = torch.stack([state_dict.pop(k) for k in keys])
+
+    @property
+    def last_expert_compute_ms(self) -> float:
+        """Time of the last forward's expert FFN compute (the grouped GEMMs, or the per-expert module calls),
+        measured with device events on the launch stream (moe_layer.py L:326-337 times the same span with the
+        host clock).  Reading it waits for the GPU to finish that span."""
+        t = self._expert_timer
+        if t is not None:
+            self._expert_timer = None
+            self._expert_ms = t.elapsed_ms()
+        return self._expert_ms
+
+    @last_expert_compute_ms.setter
+    def last_expert_compute_ms(self, v: float) -> None:
+        self._expert_timer = None
+        self._expert_ms = float(v)
 
     @property
     def last_dropped_token_fraction(self) -> float:
@@ -240,9 +283,12 @@ class DistributedMoELayer(nn.Module):
         if self._fused():
             train = torch.is_grad_enabled() and any(
                 t.requires_grad for t in (flat, weights, self.w_gate, self.w_up, self.w_down))
-            out = ExpertsFn.apply(flat, weights, self.w_gate, self.w_up, self.w_down, p, train)
+            timer = _ExpertTimer.new(flat)
+            out = ExpertsFn.apply(flat, weights, self.w_gate, self.w_up, self.w_down, p, train, timer)
         else:
-            out = self._forward_per_expert(flat, weights, p)
+            timer = _ExpertTimer.new(flat)
+            out = self._forward_per_expert(flat, weights, p, timer)
+        self._expert_timer = timer
         if self.check_numerics:
             assert not torch.isnan(out).any(), (
                 "NaN detected in DistributedMoELayer output after combine step. "
@@ -288,15 +334,20 @@ class DistributedMoELayer(nn.Module):
         out = ops.combine(y, weights, p)
         return out.reshape(shape)
 
-    def _forward_per_expert(self, flat: torch.Tensor, weights: torch.Tensor, p: ops.Plan) -> torch.Tensor:
+    def _forward_per_expert(self, flat: torch.Tensor, weights: torch.Tensor, p: ops.Plan,
+                            timer: Optional["_ExpertTimer"] = None) -> torch.Tensor:
         """Dispatch/combine kernels around per-expert module calls (custom experts, non-bf16 dtypes)."""
         xp = PermuteFn.apply(flat, p)
         offs = p.offsets.tolist()  # segment bounds for the per-expert calls
         parts = []
+        if timer is not None:
+            timer.start()
         for i, expert in enumerate(self.experts):
             lo, hi = offs[i], offs[i + 1]
             if lo < hi:
                 parts.append(expert(xp[lo:hi]))
+        if timer is not None:
+            timer.stop()
         tail = p.rows - offs[len(self.experts)]
         if tail > 0:
             parts.append(xp.new_zeros((tail, xp.shape[1])))

@@ -114,6 +114,28 @@ def test_profile_times_the_router_kernels():
         <= 1e-6 * report["achieved_bw"]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["fused", "per_expert"])
+def test_layer_times_the_expert_compute(dtype):
+    """last_expert_compute_ms: device events around the expert FFN compute (moe_layer.py L:326-337 times the
+    same span): positive, below the whole forward's time, and resolved once."""
+    from pkg.distributed.parallel_mesh import DistributedMoELayer, build_topology
+
+    say(f"[expert timing] {dtype}")
+    layer = DistributedMoELayer(256, 512, 8, 2, build_topology(), dtype=dtype).to(dev())
+    x = _tokens(1024, 256, seed=11, dtype=dtype)
+    layer(x)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    layer(x)
+    b.record()
+    ms = layer.last_expert_compute_ms
+    torch.cuda.synchronize()
+    assert 0.0 < ms <= a.elapsed_time(b) * 1.01 + 1e-3
+    assert layer.last_expert_compute_ms == ms
+    layer.last_expert_compute_ms = 0.0
+    assert layer.last_expert_compute_ms == 0.0
+
+
 def test_force_reference_is_not_shipped():
     x = _tokens(8, 16, seed=7)
     gw = torch.zeros(16, 4, device=dev())
