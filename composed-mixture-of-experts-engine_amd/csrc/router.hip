@@ -71,6 +71,14 @@ __device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int 
   for (int nt = 0; nt < NT; ++nt) pacc[nt] = 0.f;
   float zacc = 0.f;
   int nf = 0;
+  // the lane's bias values, loaded once (a wave-uniform branch on bias: no per-token load or wait)
+  float bv[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) bv[nt] = 0.f;
+  if (bias != nullptr) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bv[nt] = bias[min(nt * 16 + n, E - 1)];
+  }
   // The row of 16 lanes g owns tokens t0 + 4g + i, i < 4; the four tokens are processed side by side
   // (independent dependency chains for the scheduler to interleave).
   float lg[4][NT], m[4], inv[4];
@@ -83,7 +91,7 @@ __device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int 
     for (int nt = 0; nt < NT; ++nt) {
       const int e = nt * 16 + n;
       float v = acc[nt][i];
-      if (bias != nullptr && e < E) v += bias[e];
+      if (bias != nullptr && e < E) v += bv[nt];
       if (valid && e < E) {
         logits_out[(int64_t)tt * E + e] = v;
         if (!isfinite(v)) ++nf;
@@ -894,6 +902,65 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
   }
 }
 
+// G of one token from values already in registers (one lane per token): lg[e] = the token's logits (-inf past
+// E), f[e] = its expert's dispatch fraction (cnt * inv_nk; 0 without the aux term), and the token's top-k ids and
+// upstream weight gradients (K <= KR).  The same arithmetic as glogit_token<1, EPL>.
+template <int EPL, int KR>
+__device__ __forceinline__ void glogit_token_regs(const float (&lg)[EPL], const float (&f)[EPL], const int (&ik)[KR],
+                                                  const float (&gk)[KR], bool has_gw, const GCoef& c, int K,
+                                                  float (&gl)[EPL]) {
+  float p[EPL], gp[EPL];
+  float m = lg[0];
+#pragma unroll
+  for (int j = 1; j < EPL; ++j) m = fmaxf(m, lg[j]);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    p[j] = expf(lg[j] - m);
+    s += p[j];
+    gp[j] = 0.f;
+  }
+  const float inv = 1.f / s;
+  const float lse = m + logf(s);
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) p[j] *= inv;
+  if (has_gw) {
+    float v[KR], S = 0.f, gwv = 0.f;
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+      float vk = 0.f;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) vk = (ik[k] == j) ? p[j] : vk;
+      v[k] = k < K ? vk : 0.f;
+      S += v[k];
+      gwv += (k < K ? gk[k] : 0.f) * v[k];
+    }
+    S = fmaxf(S, 1e-30f);
+    const float iS = 1.f / S;
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+      const float gv = gk[k] * iS - gwv * iS * iS;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (k < K && ik[k] == j) gp[j] += gv;
+    }
+  }
+  float inner = 0.f, pf = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    inner += gp[j] * p[j];
+    pf += p[j] * f[j];
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    float v = p[j] * (gp[j] - inner);
+    if (c.ca != 0.f) v += c.ca * p[j] * (f[j] - pf);
+    if (c.cz != 0.f) v += c.cz * lse * p[j];
+    gl[j] = v;
+  }
+}
+
+
 // ---------------------------------------------------------------------------
 // Backward 1: G = dL/dlogits.  LPT lanes per token (EPL experts per lane).
 // Writes G (f32) and, when gb != nullptr, G rounded to bf16 in a zero-padded
@@ -1104,11 +1171,12 @@ __global__ __launch_bounds__(256) void k_router_dxdw_bf16(const uint16_t* __rest
 // prefetched two steps ahead with clamped (branch-free) loads; rows past the chunk read as zero.
 // ---------------------------------------------------------------------------
 constexpr int kSTC = 256;   // max tokens per chunk (a multiple of 64)
+constexpr int kGRegK = 4;   // top-k widths whose ids and upstream gradients the streaming backward preloads
 constexpr int kSXP = 72;    // pitch (bf16) of a wave's 32 x 64 tile: 144 bytes, conflict-free for the reads below
 typedef short sh4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) sh4 lds_sh4;
 
-template <int NTE>
+template <int NTE, int EL = NTE * 16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 4 : 1))) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ wg,
                                                             const float* __restrict__ logits,
@@ -1151,23 +1219,67 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
       r[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xw + (int64_t)min(t, tend - 1) * H));
     }
   };
+  // ---- G = dL/dlogits of the chunk, one token per thread, rounded to bf16 as the reference does
+  // (grad_logits.to(tokens.dtype)) and staged in both layouts; rows past the chunk are 0.  The token's
+  // logits, top-k ids and upstream gradients are requested first (clamped, branch-free loads), then the x
+  // prefetch, so the small loads are not queued behind the stream; with K > kGRegK the loads happen
+  // inside glogit_token instead. ----
+  // EL (<= NTE * 16): experts a token's G is computed over (8 when E <= 8)
+  const GCoef cf = glogit_coef(grad_aux, grad_z, aux_coef, z_coef, N, E, K);
+  const int r = tid;  // blockDim == kSTC >= the chunk's rounded-up row count
+  const int t = tbeg + r;
+  const int tc = min(t, tend - 1);
+  const bool regs = K <= kGRegK;
+  // raw loads only (no conversion of a loaded value before the x prefetch is issued: using one would wait
+  // for it here); the branches are wave-uniform
+  float lgv[EL];
+  int ikv[kGRegK];
+  uint32_t gkraw[kGRegK];
+  const bool gw16 = gw_dt == MOE_BF16;
+  if (regs) {
+#pragma unroll
+    for (int e = 0; e < EL; ++e) lgv[e] = logits[(int64_t)tc * E + min(e, E - 1)];
+#pragma unroll
+    for (int k = 0; k < kGRegK; ++k) ikv[k] = (int)idx[(int64_t)tc * K + min(k, K - 1)];
+    if (gw != nullptr && gw16) {
+#pragma unroll
+      for (int k = 0; k < kGRegK; ++k) gkraw[k] = static_cast<const uint16_t*>(gw)[(int64_t)tc * K + min(k, K - 1)];
+    } else if (gw != nullptr) {
+#pragma unroll
+      for (int k = 0; k < kGRegK; ++k)
+        gkraw[k] = static_cast<const uint32_t*>(gw)[(int64_t)tc * K + min(k, K - 1)];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kGRegK; ++k) gkraw[k] = 0u;
+    }
+  }
   u32x4 xa[4], xb[4];
   load_x(xa, tbeg);
   load_x(xb, tbeg + 32);
-
-  // ---- G = dL/dlogits of the chunk, one token per thread (the x prefetch above is in flight meanwhile),
-  // rounded to bf16 as the reference does (grad_logits.to(tokens.dtype)) and staged in both layouts; rows
-  // past the chunk are 0 ----
   {
-    const GCoef cf = glogit_coef(grad_aux, grad_z, aux_coef, z_coef, N, E, K);
-    const int r = tid;  // blockDim == kSTC >= the chunk's rounded-up row count
-    const int t = tbeg + r;
-    float gl[NTE * 16];
+    float gl[EL];
     if (t < tend) {
-      glogit_token<1, NTE * 16>(logits, idx, gw, gw_dt, cnt, cf, t, E, K, 0, gl);
+      if (regs) {
+        float fv[EL];
+#pragma unroll
+        for (int e = 0; e < EL; ++e) {
+          lgv[e] = e < E ? lgv[e] : -INFINITY;
+          fv[e] = 0.f;
+        }
+        if (cf.ca != 0.f) {  // the dispatch fractions (the aux term only)
+#pragma unroll
+          for (int e = 0; e < EL; ++e) fv[e] = e < E ? (float)cnt[min(e, E - 1)] * cf.inv_nk : 0.f;
+        }
+        float gkv[kGRegK];
+#pragma unroll
+        for (int k = 0; k < kGRegK; ++k) gkv[k] = __uint_as_float(gw16 ? gkraw[k] << 16 : gkraw[k]);
+        glogit_token_regs<EL, kGRegK>(lgv, fv, ikv, gkv, gw != nullptr, cf, K, gl);
+      } else {
+        glogit_token<1, EL>(logits, idx, gw, gw_dt, cnt, cf, t, E, K, 0, gl);
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < NTE * 16; ++e) gl[e] = 0.f;
+      for (int e = 0; e < EL; ++e) gl[e] = 0.f;
     }
     if (r < nst * 32) {
 #pragma unroll
@@ -1176,14 +1288,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int e0 = c8 + 2 * j, e1 = e0 + 1;
-          const float v0 = (e0 < NTE * 16 && e0 < E) ? gl[e0 < NTE * 16 ? e0 : 0] : 0.f;
-          const float v1 = (e1 < NTE * 16 && e1 < E) ? gl[e1 < NTE * 16 ? e1 : 0] : 0.f;
+          const float v0 = (e0 < EL && e0 < E) ? gl[e0 < EL ? e0 : 0] : 0.f;
+          const float v1 = (e1 < EL && e1 < E) ? gl[e1 < EL ? e1 : 0] : 0.f;
           w[j] = pack2bf(v0, v1);
         }
         *reinterpret_cast<u32x4*>(&gs[r * GP + c8]) = w;
       }
 #pragma unroll
-      for (int e = 0; e < NTE * 16; ++e) gts[e * GTP + r] = e < E ? f2bf(gl[e]) : (uint16_t)0;
+      for (int e = 0; e < NTE * 16; ++e) gts[e * GTP + r] = (e < EL && e < E) ? f2bf(gl[e < EL ? e : 0]) : (uint16_t)0;
       // the first column block of each chunk also hands G (bf16, g_pitch <= 16 expert slots) to the caller
       if (g_out != nullptr && ht == 0 && t < tend) {
         for (int c8 = 0; c8 < g_pitch; c8 += 8)
@@ -1694,6 +1806,14 @@ void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, co
                         float aux_coef, float z_coef, int N, int H, int E, int K, int tc_len, int nchunk, uint16_t* dx,
                         float* ws, uint16_t* g_out = nullptr, int g_pitch = 0) {
   const int nht = H / 256;
+  if constexpr (NTE == 1) {
+    if (E <= 8) {  // G over 8 expert slots: fewer registers while the first x tiles are in flight
+      MOE_LAUNCH(dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16", (k_router_dxdw_stream<1, 8>),
+                 dim3((unsigned)(nchunk * nht)), dim3(256), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z,
+                 aux_coef, z_coef, N, H, E, K, tc_len, nht, dx, ws, g_out, g_pitch);
+      return;
+    }
+  }
   MOE_LAUNCH(dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)),
              dim3(256), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K, tc_len,
              nht, dx, ws, g_out, g_pitch);
