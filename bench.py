@@ -13,6 +13,7 @@ timing starts; ``moe_mi355/configs.py``):
           under its own key: "router" (C2), "c1", "norm_router", "fp8_fwd",
           "dispatch" (C3) and "skewed" (C5), each with its roofline and,
           where the config has one, its CPU baseline.
+  c4      the headline C4 leg alone.
   router  C2: router fwd+bwd, T=16384 d=4096 E=8 K=2.
   c1      C1: router fwd+bwd, T=4096 d=512 E=8 K=2, fp32, aux 0.01 + z 1e-3,
           timed the reference's way (3 warmup + 20 timed, mean +- std), beside
@@ -673,7 +674,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="layer", choices=["layer", "router", "c1", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
+    ap.add_argument("--workload", default="layer", choices=["layer", "c4", "router", "c1", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
     ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -727,6 +728,17 @@ def main():
             extra["skewed"]["cpu_baseline"] = cpu_baseline_layer(torch, configs.C5, "routed", inp5, sample_T=64,
                                                                  budget_s=6.0, min_reps=2)
         del inp5
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        add_mfma_ceiling(roof, extra, fp8=False)
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
+        config["layout"] = args.layout
+    elif args.workload == "c4":
+        # the headline leg alone (as in the default run)
+        inp = configs.layer_inputs(configs.C4)
+        main_res = run_layer(args, torch, configs.C4, args.layout, inp, default_numerics=True)
+        cpu = cpu_baseline_layer(torch, configs.C4, args.layout, inp) if with_cpu else None
+        del inp
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
         add_mfma_ceiling(roof, extra, fp8=False)
