@@ -36,7 +36,7 @@ constexpr int kPlanIB = 2048;  // items per planner block
 // outside the planner's tables (the router only produces ids in range).
 __device__ __forceinline__ int clamp_e(int64_t v, int E) { return (int)min(max(v, (int64_t)0), (int64_t)(E - 1)); }
 
-__host__ __device__ inline int nbits_of(int nkeys) {
+__host__ __device__ __attribute__((always_inline)) inline int nbits_of(int nkeys) {
   int b = 0;
   while ((1 << b) < nkeys) ++b;
   return b;
@@ -47,7 +47,8 @@ __host__ __device__ inline int nbits_of(int nkeys) {
 // one per wave (waves past nwr idle: nwr shrinks with the key count so the per-wave key counts fit in LDS).
 //   pass 1  each wave walks its part in chunks of 64 and counts its items per key: lanes with equal keys
 //           are found with log2(nkeys) ballots (bit-split match); the lowest lane of each key group adds
-//           the group's size to cnt[w][key] (one writer per key per chunk: no atomics)
+//           the group's size to cnt[w][key] (an LDS integer add not waited on: the sums do not depend on
+//           the order)
 //   prefix  per key, exclusive prefix of cnt[.][key] over the waves (tot[key] = the range's total)
 //   pass 2  each wave walks its part again: an item's rank among the range's items of its key is
 //           cnt[w][key] (running) + its rank among the equal-keyed lanes of its chunk
@@ -57,7 +58,7 @@ constexpr int kPlanNT = 1024;            // threads of a planner block (16 waves
 constexpr int kPlanSmall = 16384;        // largest item count the single-block planner takes
 constexpr int kPlanCntInts = 24576;      // LDS ints of the per-wave key counts (96 KB)
 
-__host__ __device__ constexpr int plan_nwr(int nkeys) {
+__host__ __device__ __attribute__((always_inline)) constexpr int plan_nwr(int nkeys) {
   int w = 16;
   while (w > 1 && w * nkeys > kPlanCntInts) w >>= 1;
   return w;
@@ -130,7 +131,7 @@ __device__ __forceinline__ void load_keys(WaveKeys& wk, int64_t beg, int64_t end
   }
 }
 
-// pass 1 (wave w < nwr): cnt[w * nkeys + key] = items of the wave's part with that key
+// pass 1 (wave w < nwr): cnt[w * nkeys + key] = items of the wave's part with that key (cnt starts zeroed)
 __device__ __forceinline__ void group_count(const WaveKeys& wk, int w, int lane, int nkeys, int nbits, int* cnt) {
   const uint64_t lt = lane ? ((~0ull) >> (64 - lane)) : 0ull;
 #pragma unroll
@@ -139,19 +140,23 @@ __device__ __forceinline__ void group_count(const WaveKeys& wk, int w, int lane,
       const int key = wk.key[c];
       const bool valid = key >= 0;
       const uint64_t m = key_match(valid, key, nbits);
-      if (valid && (m & lt) == 0) cnt[w * nkeys + key] += __popcll(m);
+      if (valid && (m & lt) == 0) atomicAdd(&cnt[w * nkeys + key], __popcll(m));  // no return: not waited on
     }
   }
 }
 
-// prefix: cnt[w][key] <- sum_{w' < w} cnt[w'][key]; tot[key] <- sum over all waves (tot may be null)
+// prefix: cnt[w][key] <- sum_{w' < w} cnt[w'][key]; tot[key] <- sum over all waves (tot may be null).  A key's
+// nwr <= 16 counts are read before any is written.
 __device__ __forceinline__ void group_prefix(int nwr, int nkeys, int* cnt, int* tot) {
   for (int key = threadIdx.x; key < nkeys; key += blockDim.x) {
+    int v[16];
+#pragma unroll
+    for (int w = 0; w < 16; ++w) v[w] = w < nwr ? cnt[w * nkeys + key] : 0;
     int run = 0;
-    for (int w = 0; w < nwr; ++w) {
-      const int v = cnt[w * nkeys + key];
-      cnt[w * nkeys + key] = run;
-      run += v;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      if (w < nwr) cnt[w * nkeys + key] = run;
+      run += v[w];
     }
     if (tot) tot[key] = run;
   }
@@ -179,9 +184,33 @@ __device__ __forceinline__ void group_rank(const WaveKeys& wk, int w, int lane, 
   }
 }
 
-// exclusive prefix of tot[0..n) into off[0..n] (off[n] = total) by one 1024-thread block; part: LDS [1024]
+// exclusive prefix of tot[0..n) into off[0..n] (off[n] = total), ending with a block barrier.  Up to 1024 keys
+// wave 0 does it alone (at most 16 keys per lane, one wave scan, no barrier inside); beyond, the whole
+// 1024-thread block (part: LDS [1024]).
 __device__ __forceinline__ void block_excl_scan(const int* tot, int n, int* off, int* part) {
   const int tid = threadIdx.x;
+  if (n <= 64 * 16) {
+    if (tid < 64) {
+      const int per = (n + 63) / 64;
+      const int k0 = min(n, tid * per), k1 = min(n, k0 + per);
+      int sum = 0;
+      for (int k = k0; k < k1; ++k) sum += tot[k];
+      int incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (tid >= o) incl += t;
+      }
+      int run = incl - sum;
+      for (int k = k0; k < k1; ++k) {
+        off[k] = run;
+        run += tot[k];
+      }
+      if (tid == 63) off[n] = incl;
+    }
+    __syncthreads();
+    return;
+  }
   const int per = (n + kPlanNT - 1) / kPlanNT;
   const int k0 = min(n, tid * per), k1 = min(n, k0 + per);
   int sum = 0;
@@ -217,15 +246,20 @@ __device__ __forceinline__ int block_sum(int v, int* red) {
 // Largest item count of one wave-split range (the part of a wave holds at most kPlanCh chunks of 64).
 __host__ __device__ inline int64_t plan_range_max(int nkeys) { return (int64_t)plan_nwr(nkeys) * 64 * kPlanCh; }
 
-// ints of the per-wave key count table of the single-block planner (its capacity and layout groupings)
-__host__ __device__ inline int plan_small_cnt(int nk_max, int E) {
-  const int a = plan_nwr(nk_max) * nk_max, b = plan_nwr(E) * E;
+// LDS of the single-block planner (ints).  The capacity grouping's per-wave counts [nwr(K*E) * K*E] start at 0;
+// the layout grouping's arrays -- cnt [nwr(E) * E], tot [E], off [E + 1], part [1024], red [16] -- and the row
+// table staged for coalesced stores [M] follow them in the same space once the capacity pass is done.
+__host__ __device__ inline int plan_small_base(int E) { return plan_nwr(E) * E + 2 * E + 1 + kPlanNT + 16; }
+__host__ __device__ inline int64_t plan_small_lds_ints(int64_t M, int K, int E, bool drops) {
+  const int64_t a = drops ? (int64_t)plan_nwr(K * E) * K * E : 0;
+  const int64_t b = plan_small_base(E) + M;
   return a > b ? a : b;
 }
 
 // The single-block planner takes N*K <= kPlanSmall items when every grouping's range fits its waves.
-__host__ __device__ inline bool plan_small_ok(int64_t M, int nk_max, int E) {
-  return M <= kPlanSmall && M <= plan_range_max(nk_max) && M <= plan_range_max(E);
+__host__ __device__ inline bool plan_small_ok(int64_t M, int K, int E, bool drops) {
+  return M <= kPlanSmall && (!drops || M <= plan_range_max(K * E)) && M <= plan_range_max(E) &&
+         plan_small_lds_ints(M, K, E, drops) * 4 <= 160 * 1024;
 }
 
 // Rank callbacks of the layouts, shared by the single-block and the multi-block planner.  koff: key offsets;
@@ -242,49 +276,67 @@ struct RefOut {  // REFSORT: token t at position j of the stable sort of column 
   }
 };
 
-// The whole plan in one block, for plan_small_ok(N*K): capacity drops (optional), then the reference or the
-// routed row layout, all tables in LDS.  LDS: cnt [plan_small_cnt] + tot [nkeys] + off [nkeys + 1] +
-// part [1024] + red [16] ints, nkeys = K*E with drops, E otherwise.
+// The whole plan in one block, for plan_small_ok: capacity drops (optional), then the reference or the routed
+// row layout, every table in LDS (plan_small_lds_ints).  The row table's ranks scatter over M rows, so its
+// entries are staged in LDS and stored in order at the end (16-byte stores); slot_row is written in item order.
 __global__ __launch_bounds__(kPlanNT) void k_plan_small(const int64_t* __restrict__ idx, int N, int K, int E,
                                                         int64_t capacity, int layout, uint8_t* __restrict__ drop,
                                                         int* __restrict__ row_slot, int* __restrict__ slot_row,
                                                         int* __restrict__ offsets, int* __restrict__ ndrop) {
   extern __shared__ int lds[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t M = (int64_t)N * K;
-  const int nk_max = capacity >= 0 ? K * E : E;
+  const int M = N * K;  // <= kPlanSmall
+  const int nkeys = E, nwr = plan_nwr(E), nbits = nbits_of(E);
   int* cnt = lds;
-  int* tot = cnt + plan_small_cnt(nk_max, E);
-  int* off = tot + nk_max;
-  int* part = off + nk_max + 1;
+  int* tot = cnt + nwr * nkeys;
+  int* off = tot + nkeys;
+  int* part = off + nkeys + 1;
   int* red = part + kPlanNT;
+  int* stage = red + 16;
   PlanKeys pk{idx, capacity >= 0 ? drop : nullptr, K, E};
-  int dropped = 0;
   WaveKeys wk;
   if (capacity >= 0) {
-    const int nkeys = K * E, nwr = plan_nwr(nkeys), nbits = nbits_of(nkeys);
-    if (w < nwr) load_keys(wk, 0, M, nwr, w, lane, pk, kCapacity);
-    for (int q = threadIdx.x; q < nwr * nkeys; q += kPlanNT) cnt[q] = 0;
+    int* ccnt = lds;
+    const int cnk = K * E, cnw = plan_nwr(cnk), cnb = nbits_of(cnk);
+    if (w < cnw) load_keys(wk, 0, M, cnw, w, lane, pk, kCapacity);
+    for (int q = threadIdx.x; q < cnw * cnk; q += kPlanNT) ccnt[q] = 0;
     __syncthreads();
-    if (w < nwr) group_count(wk, w, lane, nkeys, nbits, cnt);
+    if (w < cnw) group_count(wk, w, lane, cnk, cnb, ccnt);
     __syncthreads();
-    group_prefix(nwr, nkeys, cnt, nullptr);
+    group_prefix(cnw, cnk, ccnt, nullptr);
     __syncthreads();
-    if (w < nwr)
-      group_rank(wk, w, lane, nkeys, nbits, cnt,
+    int dropped = 0;
+    if (w < cnw)
+      group_rank(wk, w, lane, cnk, cnb, ccnt,
                  [&](int64_t i, int, int rank) {
                    const bool d = (int64_t)rank >= capacity;
                    drop[i] = d ? 1 : 0;
                    dropped += d ? 1 : 0;
                  },
                  [](int64_t) {});
-    __syncthreads();  // the drops are visible to the whole block (workgroup-scope fence)
+    __syncthreads();  // the drops are visible to the whole block (workgroup-scope fence); ccnt is dead
+    const int total_dropped = block_sum(dropped, red);
+    if (threadIdx.x == 0) ndrop[0] = total_dropped;
+  } else if (threadIdx.x == 0) {
+    ndrop[0] = 0;
   }
-  const int total_dropped = block_sum(dropped, red);
-  if (threadIdx.x == 0) ndrop[0] = total_dropped;
-  const int nkeys = E, nwr = plan_nwr(E), nbits = nbits_of(E);
-  const int64_t nitems = layout == 0 ? N : M;
-  if (w < nwr) load_keys(wk, 0, nitems, nwr, w, lane, pk, layout == 0 ? kRefSort : kRouted);
+  const int nitems = layout == 0 ? N : M;
+  const int lmode = layout == 0 ? kRefSort : kRouted;
+  // item i takes position pos of the grouping: the reference layout gives token i (a position of the stable
+  // sort of column 0) rows pos*K .. pos*K+K-1; the routed layout gives slot i row pos
+  auto place = [&](int64_t i, int pos) {
+    if (layout == 0) {
+      for (int k = 0; k < K; ++k) {
+        stage[pos * K + k] = (int)i * K + k;
+        slot_row[i * K + k] = pos * K + k;
+      }
+    } else {
+      stage[pos] = (int)i;
+      slot_row[i] = pos;
+    }
+  };
+  auto skip = [&](int64_t i) { slot_row[i] = -1; };  // a dropped slot (routed layout)
+  if (w < nwr) load_keys(wk, 0, nitems, nwr, w, lane, pk, lmode);
   for (int q = threadIdx.x; q < nwr * nkeys; q += kPlanNT) cnt[q] = 0;
   __syncthreads();
   if (w < nwr) group_count(wk, w, lane, nkeys, nbits, cnt);
@@ -292,24 +344,107 @@ __global__ __launch_bounds__(kPlanNT) void k_plan_small(const int64_t* __restric
   group_prefix(nwr, nkeys, cnt, tot);
   __syncthreads();
   block_excl_scan(tot, nkeys, off, part);
+  if (w < nwr)
+    group_rank(wk, w, lane, nkeys, nbits, cnt, [&](int64_t i, int key, int rank) { place(i, off[key] + rank); },
+               skip);
+  __syncthreads();  // the staged row table and the key offsets are complete
   if (layout == 0) {
-    const RefOut ro{K, row_slot, slot_row};
-    if (w < nwr)
-      group_rank(wk, w, lane, nkeys, nbits, cnt, [&](int64_t t, int key, int rank) { ro(t, off[key] + rank); },
-                 [](int64_t) {});
-    const int64_t chunk = max((int64_t)1, M / E);  // E equal chunks; rows past E*chunk are never computed
-    for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = (int)min((int64_t)e * chunk, M);
+    const int64_t chunk = max((int64_t)1, (int64_t)M / E);  // E equal chunks; rows past E*chunk are never computed
+    for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = (int)min((int64_t)e * chunk, (int64_t)M);
   } else {
-    if (w < nwr)
-      group_rank(wk, w, lane, nkeys, nbits, cnt,
-                 [&](int64_t i, int key, int rank) {
-                   const int row = off[key] + rank;
-                   row_slot[row] = (int)i;
-                   slot_row[i] = row;
-                 },
-                 [&](int64_t i) { slot_row[i] = -1; });
     for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = off[e];
-    for (int64_t r = off[E] + threadIdx.x; r < M; r += kPlanNT) row_slot[r] = -1;  // no row past the kept ones
+  }
+  const int kept = layout == 0 ? M : off[E];  // rows past the kept ones (routed layout) have no slot: -1
+  if ((reinterpret_cast<uintptr_t>(row_slot) & 15u) == 0) {
+    for (int r = 4 * (int)threadIdx.x; r < M; r += 4 * kPlanNT) {
+      if (r + 4 <= M) {
+        int4 v;
+        v.x = r < kept ? stage[r] : -1;
+        v.y = r + 1 < kept ? stage[r + 1] : -1;
+        v.z = r + 2 < kept ? stage[r + 2] : -1;
+        v.w = r + 3 < kept ? stage[r + 3] : -1;
+        *reinterpret_cast<int4*>(row_slot + r) = v;
+      } else {
+        for (int q = r; q < M; ++q) row_slot[q] = q < kept ? stage[q] : -1;
+      }
+    }
+  } else {
+    for (int r = threadIdx.x; r < M; r += kPlanNT) row_slot[r] = r < kept ? stage[r] : -1;
+  }
+}
+
+// Few keys without capacity drops (E <= kPlanByKey, N*K <= kPlanSmall): block k of E places the items whose key
+// is k, so the grouping runs on E CUs at once.  Every block loads all the keys (16 waves, coalesced; L2 serves
+// all but the first block), counts per wave the items with a smaller key (-> the key's offset) and those with
+// key k (-> each wave's base), then ranks its items chunk by chunk with one ballot: rank = offset + wave base +
+// earlier chunks + lower lanes.  Item order is (wave, chunk, lane), so the ranks are the stable order.  Block k
+// writes only its own rows (a contiguous range of row_slot) and its items' slot_row entries.
+constexpr int kPlanByKey = 16;
+__global__ __launch_bounds__(kPlanNT) void k_plan_bykey(const int64_t* __restrict__ idx, int N, int K, int E,
+                                                        int layout, int* __restrict__ row_slot,
+                                                        int* __restrict__ slot_row, int* __restrict__ offsets,
+                                                        int* __restrict__ ndrop) {
+  __shared__ int s_lt[kPlanNT / 64], s_eq[kPlanNT / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int key = blockIdx.x;
+  const int M = N * K;
+  const int nitems = layout == 0 ? N : M;
+  const PlanKeys pk{idx, nullptr, K, E};
+  WaveKeys wk;
+  load_keys(wk, 0, nitems, kPlanNT / 64, w, lane, pk, layout == 0 ? kRefSort : kRouted);
+  int lt = 0, eq = 0;
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) {
+    if (c < wk.nch) {  // wave-uniform
+      const int kc = wk.key[c];
+      lt += __popcll(__ballot(kc >= 0 && kc < key));
+      eq += __popcll(__ballot(kc == key));
+    }
+  }
+  if (lane == 0) {
+    s_lt[w] = lt;
+    s_eq[w] = eq;
+  }
+  __syncthreads();
+  int off = 0, run = 0;
+#pragma unroll
+  for (int q = 0; q < kPlanNT / 64; ++q) {
+    off += s_lt[q];
+    run += q < w ? s_eq[q] : 0;
+  }
+  run += off;
+  const uint64_t below = lane ? ((~0ull) >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) {
+    if (c < wk.nch) {  // wave-uniform
+      const bool hit = wk.key[c] == key;
+      const uint64_t m = __ballot(hit);
+      if (hit) {
+        const int64_t i = wk.lo + 64 * c + lane;
+        const int pos = run + __popcll(m & below);
+        if (layout == 0) {
+          for (int k = 0; k < K; ++k) {
+            row_slot[pos * K + k] = (int)i * K + k;
+            slot_row[i * K + k] = pos * K + k;
+          }
+        } else {
+          row_slot[pos] = (int)i;
+          slot_row[i] = pos;
+        }
+      }
+      run += __popcll(m);
+    }
+  }
+  if (threadIdx.x == 0) {
+    if (layout == 0) {
+      const int chunk = max(1, M / E);  // E equal chunks; rows past E*chunk are never computed
+      offsets[key] = min(key * chunk, M);
+      if (key == E - 1) offsets[E] = min(E * chunk, M);
+    } else {
+      offsets[key] = off;
+      if (key == E - 1) offsets[E] = M;  // every slot is kept
+    }
+    if (key == 0) ndrop[0] = 0;
   }
 }
 
@@ -917,9 +1052,13 @@ int plan_run(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capaci
   const int64_t M = N * K;
   uint8_t* drop = capacity >= 0 ? drop_out : nullptr;
   const PlanKeys pk{idx, drop, (int)K, (int)E};
-  const int nk_max = drop ? (int)(K * E) : (int)E;
-  if (plan_small_ok(M, nk_max, (int)E)) {
-    const size_t lds = (size_t)(plan_small_cnt(nk_max, (int)E) + 2 * nk_max + 1 + kPlanNT + 16) * 4;
+  if (!drop && E <= kPlanByKey && M <= kPlanSmall) {
+    MOE_LAUNCH("k_plan_bykey", k_plan_bykey, dim3((unsigned)E), dim3(kPlanNT), 0, s, idx, (int)N, (int)K, (int)E,
+               layout, row_slot, slot_row, offsets, ndrop);
+    return check_launch("moe_plan");
+  }
+  if (plan_small_ok(M, (int)K, (int)E, drop != nullptr)) {
+    const size_t lds = (size_t)plan_small_lds_ints(M, (int)K, (int)E, drop != nullptr) * 4;
     if (int rc = plan_allow_lds(k_plan_small, lds, g_lds_small)) return rc;
     MOE_LAUNCH("k_plan_small", k_plan_small, dim3(1), dim3(kPlanNT), lds, s, idx, (int)N, (int)K, (int)E, capacity,
                layout, drop, row_slot, slot_row, offsets, ndrop);

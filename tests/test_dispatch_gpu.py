@@ -41,6 +41,12 @@ CASES = [
     (16384, 1, 1024, None, 0.0),  # single block, 1024 keys
     (1500, 8, 1024, 1.0, 2.0),  # 8192 capacity keys: too many for one block's waves at 12000 slots
     (3000, 8, 1024, 1.25, 0.0),  # the same keys over several blocks
+    # no capacity, E <= 16: one block per key
+    (8192, 2, 8, None, 0.0),  # C4 shape
+    (5000, 3, 16, None, 2.0),
+    (16384, 1, 16, None, 1.0),  # the largest per-key plan
+    (7, 2, 2, None, 0.0),
+    (16385, 1, 8, None, 0.0),  # one slot more: the multi-block planner without drops
 ]
 
 
