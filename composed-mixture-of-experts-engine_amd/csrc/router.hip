@@ -194,6 +194,157 @@ __device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int 
   }
 }
 
+// Routing of a block's 16*TG tokens with one lane per token (E <= EP, EP = 8 or 16), called by every thread of
+// the 512-thread block.  The 8 waves' partial logit tiles (s_accf: wave w's TG 16x16 tiles in MFMA layout,
+// TG*256 floats) are summed in wave order into s_lg [16*TG][17] (rows padded: the per-token reads below hit
+// distinct banks); then wave 0 routes token t0 + lane from its logits in registers: bias, the logits / lse
+// outputs, softmax, top-k (K rounds of a strict arg-max over order-preserving keys, scanned from expert 0 so the
+// lowest expert wins a tie), renormalised weights; it leaves each token's probabilities in its s_lg row and its
+// picks as a bit mask in s_pick [64].  The per-expert statistics are then spread over the waves (wave w takes
+// experts w and w + 8): pick counts by ballots, probability sums by DPP row sums and the four rows in order.
+// Results: s_cnt[e], s_p[0][e], s_z[0], s_nf[0] (zeros in s_p[q] / s_z[q] / s_nf[q], q > 0, which the block
+// tail also adds).
+template <int TG, int EP>
+__device__ __forceinline__ void route_lanes(const float* s_accf, float* s_lg, int* s_pick, int t0,
+                                            const float* __restrict__ bias, int N, int E, int K,
+                                            int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt,
+                                            float* __restrict__ logits_out, float* __restrict__ lse_out, int* s_cnt,
+                                            float (*s_p)[16], float* s_z, int* s_nf) {
+  constexpr int NV = TG * 256;
+  for (int v = threadIdx.x; v < NV; v += 512) {
+    float a = s_accf[v];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) a += s_accf[w * NV + v];
+    const int q = v >> 8, ln = (v >> 2) & 63, i = v & 3;
+    s_lg[(16 * q + 4 * (ln >> 4) + i) * 17 + (ln & 15)] = a;
+  }
+  for (int i = threadIdx.x; i < TG * 16; i += 512) {
+    if (i >= 16) s_p[i >> 4][i & 15] = 0.f;
+    if (i > 0 && i < TG) {
+      s_z[i] = 0.f;
+      s_nf[i] = 0;
+    }
+  }
+  lds_sync();
+  const int lane = threadIdx.x & 63;
+  const bool valid = lane < 16 * TG && t0 + lane < N;
+  // a row of 16 lanes sums its values, then the four row sums are added in row order
+  auto wave_total = [&](float v) __attribute__((always_inline)) {
+    v = row16_sum(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  };
+  if (threadIdx.x < 64) {
+    const int tt = t0 + lane;
+    float* const row = s_lg + min(lane, 16 * TG - 1) * 17;
+    float lg[EP];
+    int nf = 0;
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+      float v = row[e];
+      if (e < E) {
+        if (bias != nullptr) v += bias[e];  // wave-uniform address: scalar loads
+        nf += (valid && !isfinite(v)) ? 1 : 0;
+      }
+      lg[e] = v;
+    }
+    if (valid) {
+      float* lrow = logits_out + (int64_t)tt * E;
+      if ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(logits_out) & 15u) == 0) {
+#pragma unroll
+        for (int e = 0; e < EP; e += 4)
+          if (e < E) *reinterpret_cast<f32x4*>(lrow + e) = f32x4{lg[e], lg[e + 1], lg[e + 2], lg[e + 3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < EP; ++e)
+          if (e < E) lrow[e] = lg[e];
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+      float v = lg[e];
+      if (v != v || e >= E) v = -INFINITY;  // NaN never wins a top-k slot
+      lg[e] = v;
+      m = fmaxf(m, v);
+    }
+    float ex[EP], sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+      ex[e] = expf(lg[e] - m);
+      sum += ex[e];
+    }
+    const float inv = 1.f / sum;
+    const float lse = m + logf(sum);
+    if (valid) lse_out[tt] = lse;
+    uint32_t kh[EP];
+#pragma unroll
+    for (int e = 0; e < EP; ++e) kh[e] = e < E ? order_key(lg[e]) : 0u;
+    uint32_t pick = 0u;
+    float psum = 0.f;
+    int se[EP];
+    float sp[EP];
+#pragma unroll
+    for (int r = 0; r < EP; ++r) {
+      se[r] = 0;
+      sp[r] = 0.f;
+      if (r < K) {  // wave-uniform
+        uint32_t bh = 0u;
+        int be = 0;
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+          const bool t = kh[e] > bh;
+          bh = t ? kh[e] : bh;
+          be = t ? e : be;
+        }
+#pragma unroll
+        for (int e = 0; e < EP; ++e) kh[e] = e == be ? 0u : kh[e];
+        const float pv = expf(order_val(bh) - m) * inv;
+        psum += pv;
+        se[r] = be;
+        sp[r] = pv;
+        pick |= 1u << be;
+      }
+    }
+    const float rden = 1.f / fmaxf(psum, 1e-30f);
+    if (valid) {
+#pragma unroll
+      for (int r = 0; r < EP; ++r) {
+        if (r < K) {
+          idx_out[(int64_t)tt * K + r] = se[r];
+          store_f(w_out, w_dt, (int64_t)tt * K + r, sp[r] * rden);
+        }
+      }
+    }
+    if (lane < 16 * TG) {
+#pragma unroll
+      for (int e = 0; e < EP; ++e) row[e] = valid ? ex[e] * inv : 0.f;  // the token's probabilities
+    }
+    s_pick[lane] = valid ? (int)pick : 0;
+    const float zs = wave_total(valid ? lse * lse : 0.f);
+    const int nfs = __ballot(nf > 0) == 0ull ? 0 : wave_sum(nf);  // the reduction only when some lane has one
+    if (lane == 0) {
+      s_z[0] = zs;
+      s_nf[0] = nfs;
+    }
+  }
+  lds_sync();
+  const int wv = threadIdx.x >> 6;
+  const int pk = s_pick[lane];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = wv + 8 * h;
+    const int c = (int)__popcll(__ballot((pk >> e) & 1));
+    const float ps = e < E ? wave_total(lane < 16 * TG ? s_lg[lane * 17 + e] : 0.f) : 0.f;
+    if (lane == 0) {
+      if (e < E) s_cnt[e] = c;
+      s_p[0][e] = ps;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Forward, bf16 x bf16, MFMA.
 //   NT: 16-expert tiles (ceil(E/16)).  HS: waves sharing one 16-token group,
@@ -426,7 +577,9 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
   constexpr int ACC = 8 * TG * NT * 64 * 16;
   constexpr int O_CNT = ACC, O_P = O_CNT + NT * 16 * 4, O_Z = O_P + TG * NT * 16 * 4, O_NF = O_Z + TG * 4;
   constexpr int O_LAST = O_NF + TG * 4, O_FIN = O_LAST + 16;
-  constexpr int EPI = O_FIN + finalize_scratch_floats<512>() * 4;
+  constexpr int O_LG = O_FIN + finalize_scratch_floats<512>() * 4;
+  constexpr int O_PICK = O_LG + 16 * TG * 17 * 4;
+  constexpr int EPI = O_PICK + (NT == 1 ? 64 * 4 : 0);
   static_assert(RING >= EPI, "ring too small for the epilogue arrays");
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING];
   f32x4(*s_acc)[TG][NT][64] = reinterpret_cast<f32x4(*)[TG][NT][64]>(ring);
@@ -516,15 +669,25 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
       for (int nt = 0; nt < NT; ++nt)
         acc[q][nt] = mfma16x16x32(__builtin_bit_cast(bf16x8, a[q]), __builtin_bit_cast(bf16x8, b[nt]), acc[q][nt]);
   }
-  __syncthreads();  // every wave is done with the ring: it now holds the partial logit tiles
+  lds_sync();  // every wave is done with the ring: it now holds the partial logit tiles
 
 #pragma unroll
   for (int q = 0; q < TG; ++q)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) s_acc[wv][q][nt][lane] = acc[q][nt];
   for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
-  __syncthreads();  // partial tiles visible, s_cnt zeroed
-  if (wv < TG) {
+  lds_sync();  // partial tiles visible, s_cnt zeroed
+  if constexpr (NT == 1) {
+    float* s_lg = reinterpret_cast<float*>(ring + O_LG);
+    int* s_pick = reinterpret_cast<int*>(ring + O_PICK);
+    const float* s_accf = reinterpret_cast<const float*>(ring);
+    if (E <= 8)
+      route_lanes<TG, 8>(s_accf, s_lg, s_pick, t0, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt,
+                         s_p, s_z, s_nf);
+    else
+      route_lanes<TG, 16>(s_accf, s_lg, s_pick, t0, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt,
+                          s_p, s_z, s_nf);
+  } else if (wv < TG) {
     f32x4 lg[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -535,7 +698,7 @@ __global__ __launch_bounds__(512) void k_router_fwd_stream(
     route_group<NT>(lg, t0 + 16 * wv, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt, s_p[wv],
                     &s_z[wv], &s_nf[wv]);
   }
-  __syncthreads();
+  lds_sync();  // the block's statistics are in LDS; the routing outputs' stores drain in the tail's wait
   fwd_block_tail<TG, NT>(s_cnt, s_p, s_z, s_nf, s_last, s_fin, N, E, K, part_cnt, part_p, part_z, ticket, aux_coef,
                          z_coef, cnt_out, stats, aux_out, z_out);
 }
