@@ -962,6 +962,10 @@ __global__ __launch_bounds__(256) void k_route_from_logits(const float* __restri
 // dL/dlogits of one token, LPT lanes per token, lane `sub` owning experts sub + LPT*j (j < EPL):
 //   softmax p, renormalised top-k weights v_k = p_{e_k} / max(sum_k p_{e_k}, 1e-30) with upstream gw,
 //   aux term ca * p (f - sum p f) with f_e = cnt_e / (N K), z term cz * lse * p.
+// The exponentials, the logarithm and the reciprocals take the hardware forms (v_exp_f32, v_log_f32,
+// v_rcp_f32: relative error ~1e-6 at these magnitudes, far below the bf16 rounding G gets before its
+// products): the full-precision library forms expand to ~15 instructions each, and in the backward's
+// prologue, run once per block on a cold instruction cache, code length is time.
 struct GCoef {
   float ca, cz, inv_nk;
 };
@@ -1015,12 +1019,12 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    p[j] = expf(lg[j] - m);
+    p[j] = __expf(lg[j] - m);
     s += p[j];
   }
   s = grp_sum<LPT>(s);
-  const float inv = 1.f / s;
-  const float lse = m + logf(s);
+  const float inv = __builtin_amdgcn_rcpf(s);
+  const float lse = m + __logf(s);
 #pragma unroll
   for (int j = 0; j < EPL; ++j) p[j] *= inv;
   if (gw != nullptr) {
@@ -1038,7 +1042,7 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
       gwv += gk * v;
     }
     S = fmaxf(S, 1e-30f);
-    const float iS = 1.f / S;
+    const float iS = __builtin_amdgcn_rcpf(S);
     for (int k = 0; k < K; ++k) {
       const int e = (int)idx[(int64_t)t * K + k];
       const float gk = load_f(gw, gw_dt, (int64_t)t * K + k);
@@ -1079,12 +1083,12 @@ __device__ __forceinline__ void glogit_token_regs(const float (&lg)[EPL], const 
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    p[j] = expf(lg[j] - m);
+    p[j] = __expf(lg[j] - m);
     s += p[j];
     gp[j] = 0.f;
   }
-  const float inv = 1.f / s;
-  const float lse = m + logf(s);
+  const float inv = __builtin_amdgcn_rcpf(s);
+  const float lse = m + __logf(s);
 #pragma unroll
   for (int j = 0; j < EPL; ++j) p[j] *= inv;
   if (has_gw) {
@@ -1099,7 +1103,7 @@ __device__ __forceinline__ void glogit_token_regs(const float (&lg)[EPL], const 
       gwv += (k < K ? gk[k] : 0.f) * v[k];
     }
     S = fmaxf(S, 1e-30f);
-    const float iS = 1.f / S;
+    const float iS = __builtin_amdgcn_rcpf(S);
 #pragma unroll
     for (int k = 0; k < KR; ++k) {
       const float gv = gk[k] * iS - gwv * iS * iS;
@@ -1339,8 +1343,12 @@ constexpr int kSXP = 72;    // pitch (bf16) of a wave's 32 x 64 tile: 144 bytes,
 typedef short sh4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) sh4 lds_sh4;
 
-template <int NTE, int EL = NTE * 16>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 4 : 1))) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
+// KR: top-k slots whose ids and upstream gradients are preloaded (K <= KR <= kGRegK; K > kGRegK reads them
+// where G is formed).  WPB: waves per block (64 hidden columns each), 4 or 16; with 16 one block fills a CU's
+// 16 wave slots, so the CU's memory requests come from one block whose waves start together (with four
+// 4-wave blocks per CU the first-dispatched block's requests are served first and the others start late).
+template <int NTE, int EL, int KR, int WPB>
+__global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 4 : 1))) void k_router_dxdw_stream(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ wg,
                                                             const float* __restrict__ logits,
                                                             const int64_t* __restrict__ idx,
@@ -1357,7 +1365,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
   constexpr int GTP = kSTC + 8;      // expert-major G row pitch
   __shared__ __attribute__((aligned(16))) uint16_t gs[kSTC * GP];
   __shared__ __attribute__((aligned(16))) uint16_t gts[NTE * 16 * GTP];
-  __shared__ __attribute__((aligned(16))) uint16_t xs[4][32 * kSXP];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[WPB][32 * kSXP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1369,7 +1377,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
   const int tbeg = chunk * tc_len;
   const int tend = min(N, tbeg + tc_len);
   const int nst = ((tend - tbeg + 63) / 64) * 2;  // 32-token steps, rounded up to even
-  const int col0 = ht * 256 + wv * 64;            // this wave's first hidden column
+  const int col0 = ht * (64 * WPB) + wv * 64;     // this wave's first hidden column
   uint16_t* xsw = xs[wv];
 
   // x stream: lane loads rows (lane/8) + 8j of the step, 16-byte chunk lane%8 of the wave's 64 columns
@@ -1392,28 +1400,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
   const int r = tid;  // blockDim == kSTC >= the chunk's rounded-up row count
   const int t = tbeg + r;
   const int tc = min(t, tend - 1);
-  const bool regs = K <= kGRegK;
+  const bool regs = KR == 2 || K <= KR;  // the KR == 2 form is only launched with K <= 2
   // raw loads only (no conversion of a loaded value before the x prefetch is issued: using one would wait
   // for it here); the branches are wave-uniform
   float lgv[EL];
-  int ikv[kGRegK];
-  uint32_t gkraw[kGRegK];
+  int ikv[KR];
+  uint32_t gkraw[KR];
   const bool gw16 = gw_dt == MOE_BF16;
-  if (regs) {
+  if (regs && wv < kSTC / 64) {  // the G waves (one token per thread)
 #pragma unroll
     for (int e = 0; e < EL; ++e) lgv[e] = logits[(int64_t)tc * E + min(e, E - 1)];
 #pragma unroll
-    for (int k = 0; k < kGRegK; ++k) ikv[k] = (int)idx[(int64_t)tc * K + min(k, K - 1)];
+    for (int k = 0; k < KR; ++k) ikv[k] = (int)idx[(int64_t)tc * K + min(k, K - 1)];
     if (gw != nullptr && gw16) {
 #pragma unroll
-      for (int k = 0; k < kGRegK; ++k) gkraw[k] = static_cast<const uint16_t*>(gw)[(int64_t)tc * K + min(k, K - 1)];
+      for (int k = 0; k < KR; ++k) gkraw[k] = static_cast<const uint16_t*>(gw)[(int64_t)tc * K + min(k, K - 1)];
     } else if (gw != nullptr) {
 #pragma unroll
-      for (int k = 0; k < kGRegK; ++k)
-        gkraw[k] = static_cast<const uint32_t*>(gw)[(int64_t)tc * K + min(k, K - 1)];
+      for (int k = 0; k < KR; ++k) gkraw[k] = static_cast<const uint32_t*>(gw)[(int64_t)tc * K + min(k, K - 1)];
     } else {
 #pragma unroll
-      for (int k = 0; k < kGRegK; ++k) gkraw[k] = 0u;
+      for (int k = 0; k < KR; ++k) gkraw[k] = 0u;
     }
   }
   u32x4 xa[4], xb[4];
@@ -1433,11 +1440,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
 #pragma unroll
           for (int e = 0; e < EL; ++e) fv[e] = e < E ? (float)cnt[min(e, E - 1)] * cf.inv_nk : 0.f;
         }
-        float gkv[kGRegK];
+        float gkv[KR];
 #pragma unroll
-        for (int k = 0; k < kGRegK; ++k) gkv[k] = __uint_as_float(gw16 ? gkraw[k] << 16 : gkraw[k]);
-        glogit_token_regs<EL, kGRegK>(lgv, fv, ikv, gkv, gw != nullptr, cf, K, gl);
-      } else {
+        for (int k = 0; k < KR; ++k) gkv[k] = __uint_as_float(gw16 ? gkraw[k] << 16 : gkraw[k]);
+        glogit_token_regs<EL, KR>(lgv, fv, ikv, gkv, gw != nullptr, cf, K, gl);
+      } else if constexpr (KR != 2) {
         glogit_token<1, EL>(logits, idx, gw, gw_dt, cnt, cf, t, E, K, 0, gl);
       }
     } else {
@@ -1470,14 +1477,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTE == 1 ? 
 
   // gate fragments for dx: B[k = e][n = h] = wg[h][e]
   i16x8 wB[4];
+  if (E == 8) {  // each gate row is one 16-byte piece (lanes past the first 8 experts hold zeros)
 #pragma unroll
-  for (int nc = 0; nc < 4; ++nc) {
-    const int h = col0 + nc * 16 + n;
+    for (int nc = 0; nc < 4; ++nc) {
+      const i16x8 v = *reinterpret_cast<const i16x8*>(wg + (int64_t)(col0 + nc * 16 + n) * 8);
+      wB[nc] = g == 0 ? v : i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = g * 8 + j;
-      wB[nc][j] = (short)wg[(int64_t)h * E + min(e, E - 1)];
-      if (e >= E) wB[nc][j] = 0;
+    for (int nc = 0; nc < 4; ++nc) {
+      const int h = col0 + nc * 16 + n;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = g * 8 + j;
+        wB[nc][j] = (short)wg[(int64_t)h * E + min(e, E - 1)];
+        if (e >= E) wB[nc][j] = 0;
+      }
     }
   }
   f32x4 accw[4][NTE];
@@ -1903,8 +1918,9 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
     p.tc_len = std::max(64, cdiv(cdiv(N, want), 64) * 64);
     p.nchunk = cdiv(N, p.tc_len);
   } else if (p.stream) {
-    // one round of blocks: four per CU with up to 16 experts (39 KB of LDS, at most 128 registers), two
-    // with more (the second expert tile's registers); chunks of a multiple of 64 tokens, at most kSTC
+    // one round of blocks: per CU four 4-wave blocks (or one 16-wave block with E <= 8 and H % 1024 == 0)
+    // with up to 16 experts (at most 128 registers), two 4-wave blocks with more (the second expert tile's
+    // registers); chunks of a multiple of 64 tokens, at most kSTC
     const int nht = (int)(H / 256);
     const int want = std::max(1, (E <= 16 ? 1024 : 512) / nht);
     p.tc_len = std::min(kSTC, std::max(64, cdiv(cdiv(N, want), 64) * 64));
@@ -1968,18 +1984,29 @@ void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, co
                         const void* gw, int gw_dt, const int64_t* cnt, const float* grad_aux, const float* grad_z,
                         float aux_coef, float z_coef, int N, int H, int E, int K, int tc_len, int nchunk, uint16_t* dx,
                         float* ws, uint16_t* g_out = nullptr, int g_pitch = 0) {
-  const int nht = H / 256;
+  const char* name = dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16";
+#define MOE_DXDW_STREAM(EL_, KR_, WPB_)                                                                               \
+  MOE_LAUNCH(name, (k_router_dxdw_stream<NTE, EL_, KR_, WPB_>), dim3((unsigned)(nchunk * (H / (64 * WPB_)))),          \
+             dim3(64 * WPB_), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K,  \
+             tc_len, H / (64 * WPB_), dx, ws, g_out, g_pitch)
+  // G over 8 expert slots when E <= 8 (fewer registers while the first x tiles are in flight); the top-k
+  // slots preloaded: 2 when K <= 2 (shorter code: the prologue runs on a cold instruction cache), else 4;
+  // 16-wave blocks (1024 columns) when H allows
   if constexpr (NTE == 1) {
-    if (E <= 8) {  // G over 8 expert slots: fewer registers while the first x tiles are in flight
-      MOE_LAUNCH(dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16", (k_router_dxdw_stream<1, 8>),
-                 dim3((unsigned)(nchunk * nht)), dim3(256), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z,
-                 aux_coef, z_coef, N, H, E, K, tc_len, nht, dx, ws, g_out, g_pitch);
+    if (E <= 8) {
+      if (H % 1024 == 0) {
+        if (K <= 2) MOE_DXDW_STREAM(8, 2, 16);
+        else MOE_DXDW_STREAM(8, kGRegK, 16);
+      } else {
+        if (K <= 2) MOE_DXDW_STREAM(8, 2, 4);
+        else MOE_DXDW_STREAM(8, kGRegK, 4);
+      }
       return;
     }
   }
-  MOE_LAUNCH(dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16", (k_router_dxdw_stream<NTE>), dim3((unsigned)(nchunk * nht)),
-             dim3(256), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K, tc_len,
-             nht, dx, ws, g_out, g_pitch);
+  if (K <= 2) MOE_DXDW_STREAM(NTE * 16, 2, 4);
+  else MOE_DXDW_STREAM(NTE * 16, kGRegK, 4);
+#undef MOE_DXDW_STREAM
 }
 
 template <int EK, int NTE>
