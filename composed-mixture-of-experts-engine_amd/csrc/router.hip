@@ -282,41 +282,31 @@ __device__ __forceinline__ void route_lanes(const float* s_accf, float* s_lg, in
     uint32_t kh[EP];
 #pragma unroll
     for (int e = 0; e < EP; ++e) kh[e] = e < E ? order_key(lg[e]) : 0u;
+    // the K rounds run as a rolled loop (short code); a round's probability waits in the token's row
     uint32_t pick = 0u;
     float psum = 0.f;
-    int se[EP];
-    float sp[EP];
+#pragma unroll 1
+    for (int r = 0; r < K; ++r) {
+      uint32_t bh = 0u;
+      int be = 0;
 #pragma unroll
-    for (int r = 0; r < EP; ++r) {
-      se[r] = 0;
-      sp[r] = 0.f;
-      if (r < K) {  // wave-uniform
-        uint32_t bh = 0u;
-        int be = 0;
-#pragma unroll
-        for (int e = 0; e < EP; ++e) {
-          const bool t = kh[e] > bh;
-          bh = t ? kh[e] : bh;
-          be = t ? e : be;
-        }
-#pragma unroll
-        for (int e = 0; e < EP; ++e) kh[e] = e == be ? 0u : kh[e];
-        const float pv = expf(order_val(bh) - m) * inv;
-        psum += pv;
-        se[r] = be;
-        sp[r] = pv;
-        pick |= 1u << be;
+      for (int e = 0; e < EP; ++e) {
+        const bool t = kh[e] > bh;
+        bh = t ? kh[e] : bh;
+        be = t ? e : be;
       }
+#pragma unroll
+      for (int e = 0; e < EP; ++e) kh[e] = e == be ? 0u : kh[e];
+      const float pv = expf(order_val(bh) - m) * inv;
+      psum += pv;
+      pick |= 1u << be;
+      if (valid) idx_out[(int64_t)tt * K + r] = be;
+      if (lane < 16 * TG) row[r] = pv;
     }
     const float rden = 1.f / fmaxf(psum, 1e-30f);
     if (valid) {
-#pragma unroll
-      for (int r = 0; r < EP; ++r) {
-        if (r < K) {
-          idx_out[(int64_t)tt * K + r] = se[r];
-          store_f(w_out, w_dt, (int64_t)tt * K + r, sp[r] * rden);
-        }
-      }
+#pragma unroll 1
+      for (int r = 0; r < K; ++r) store_f(w_out, w_dt, (int64_t)tt * K + r, row[r] * rden);
     }
     if (lane < 16 * TG) {
 #pragma unroll
