@@ -669,6 +669,46 @@ def add_mfma_ceiling(roof, extra, fp8):
     log(f"[bench] MFMA ceiling ({'fp8' if fp8 else 'bf16'}): {tf:.0f} TFLOP/s at {mhz:.0f} MHz")
 
 
+_HBM_CEILING = {}
+
+
+def hbm_ceiling(mode, nbytes):
+    """GB/s of a plain stream on this GPU (moe_prof_hbm_ceiling): mode 0 read, 1 write, 2 copy of ``nbytes``,
+    3 fan-out (``nbytes`` of 4 KB rows each read once and written 6 times).  The working set decides how much the
+    256 MB Infinity Cache serves, so each caller sizes the stream like the kernel it is compared with."""
+    from moe_mi355 import _lib
+
+    key = (mode, int(nbytes))
+    if key not in _HBM_CEILING:
+        _HBM_CEILING[key] = round(_lib.prof_hbm_ceiling(int(nbytes), mode), 1)
+    return _HBM_CEILING[key]
+
+
+def add_hbm_ceiling_dispatch(res):
+    """The permute reads the token rows once and writes each to its K rows: its practical ceiling is the fan-out
+    stream over the same rows (C3: 268 MB in, 1.6 GB out), reported beside the 8 TB/s peak."""
+    xb = res["tokens"] * res["d_model"] * 2
+    c = {"fanout6": hbm_ceiling(3, xb), "write": hbm_ceiling(1, 6 * xb), "read": hbm_ceiling(0, xb)}
+    log(f"[bench] HBM stream ceilings at C3 sizes (GB/s): {c}")
+    res["hbm_ceiling_GBps"] = c
+    roof = res["roofline"]
+    roof["ceiling"] = c["fanout6"]
+    roof["ceiling_kind"] = "fan-out stream over the same rows (each read once, written 6 times)"
+    roof["frac_of_ceiling"] = round(roof["achieved"] / c["fanout6"], 4)
+
+
+def add_hbm_ceiling_router(res):
+    """The router step reads x (forward) and reads x + writes dx (backward): its stream floor is that read at a plain
+    read stream's rate plus that copy at a plain copy stream's rate, over buffers of x's size."""
+    xb = res["tokens"] * res["d_model"] * 2
+    c = {"read": hbm_ceiling(0, xb), "copy": hbm_ceiling(2, xb)}
+    log(f"[bench] HBM stream ceilings at the router's size (GB/s): {c}")
+    res["hbm_ceiling_GBps"] = c
+    floor_us = xb / (c["read"] * 1e3) + 2 * xb / (c["copy"] * 1e3)
+    res["stream_floor_us"] = round(floor_us, 1)
+    res["graph_frac_of_stream_floor"] = round(floor_us / (res["graph_ms_per_step"] * 1e3), 4)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -720,6 +760,8 @@ def main():
             extra["router"]["cpu_baseline"] = cpu_baseline_router(torch)
         extra["dispatch"] = run_dispatch(args, torch, with_cpu=with_cpu)
         log(f"[bench] C3 dispatch: {extra['dispatch']['ms_per_step']:.4f} ms/step")
+        add_hbm_ceiling_dispatch(extra["dispatch"])
+        add_hbm_ceiling_router(extra["router"])
         log("[bench] generating C5 inputs")
         inp5 = configs.layer_inputs(configs.C5)
         extra["skewed"] = run_layer(args, torch, configs.C5, "routed", inp5)
@@ -746,6 +788,7 @@ def main():
         config["layout"] = args.layout
     elif args.workload == "router":
         main_res = run_router(args, torch)
+        add_hbm_ceiling_router(main_res)
         cpu = None if args.no_cpu_baseline else cpu_baseline_router(torch)
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")
@@ -765,6 +808,7 @@ def main():
         config = {"workload": main_res.pop("workload"), "tokens": main_res.pop("tokens")}
     elif args.workload == "dispatch":
         main_res = run_dispatch(args, torch, with_cpu=with_cpu)
+        add_hbm_ceiling_dispatch(main_res)
         cpu = main_res.pop("cpu_baseline", None)
         value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
         roof = main_res.pop("roofline")

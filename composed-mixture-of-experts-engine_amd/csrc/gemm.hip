@@ -1074,6 +1074,91 @@ __global__ __launch_bounds__(512) void k_mfma_ceiling(int iters, unsigned long l
 }
 }  // namespace moe
 
+// ---------------------------------------------------------------------------
+// HBM ceiling probe (bench only): grid-stride streams of 16-byte accesses over buffers far larger than the
+// caches, in the shapes the data-movement kernels have: read only, write only, copy, and fan-out (each
+// 4 KB row read once and written to 6 rows, as the permute does at K = 6).  Streaming cache policy
+// (non-temporal) throughout, as in those kernels.
+// ---------------------------------------------------------------------------
+namespace moe {
+__global__ __launch_bounds__(256) void k_hbm_probe(int mode, const u32x4* __restrict__ x, u32x4* __restrict__ y,
+                                                   int64_t n, unsigned* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (mode == 3) {  // fan-out: one wave per 4 KB row of x (n rows), written to rows r, r + n, ..., r + 5n of y
+    const int lane = threadIdx.x & 63;
+    for (int64_t r = t >> 6; r < n; r += stride >> 6) {
+      u32x4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = __builtin_nontemporal_load(x + r * 256 + j * 64 + lane);
+#pragma unroll
+      for (int k = 0; k < 6; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) __builtin_nontemporal_store(v[j], y + ((int64_t)k * n + r) * 256 + j * 64 + lane);
+    }
+    return;
+  }
+  unsigned acc = 0u;
+  for (int64_t i = t; i < n; i += 4 * stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t k = i + u * stride;
+      if (mode == 1) v[u] = u32x4{(unsigned)k, 1u, 2u, 3u};
+      else v[u] = k < n ? __builtin_nontemporal_load(x + k) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t k = i + u * stride;
+      if (mode == 0) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+      else if (k < n) __builtin_nontemporal_store(v[u], y + k);
+    }
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the reads live
+}
+}  // namespace moe
+
+extern "C" int moe_prof_hbm_ceiling(int64_t bytes, int mode, double* gbps) {
+  if (bytes < (1 << 20) || bytes > ((int64_t)1 << 34) || mode < 0 || mode > 3 || !gbps)
+    return fail_arg("moe_prof_hbm_ceiling: bad arguments (1 MiB <= bytes <= 16 GiB, mode 0..3, non-null output)");
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return check_launch("moe_prof_hbm_ceiling");
+  // the buffer the mode moves `bytes` through: x read (modes 0, 2, 3), y written (modes 1, 2, 3)
+  const int64_t rows = bytes / 4096;
+  const int64_t xb = mode == 1 ? 16 : (mode == 3 ? rows * 4096 : bytes);
+  const int64_t yb = mode == 0 ? 16 : (mode == 3 ? 6 * rows * 4096 : bytes);
+  const int64_t n = mode == 3 ? rows : bytes / 16;
+  const double moved = mode == 2 ? 2.0 * (double)bytes : (mode == 3 ? 7.0 * (double)rows * 4096 : (double)bytes);
+  u32x4 *x = nullptr, *y = nullptr;
+  unsigned* sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = 0;
+  float ms = 0.f;
+  if (hipMalloc(&x, (size_t)xb) != hipSuccess || hipMalloc(&y, (size_t)yb) != hipSuccess ||
+      hipMalloc(&sink, 16) != hipSuccess || hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess ||
+      hipMemsetAsync(x, 1, (size_t)xb, nullptr) != hipSuccess) {
+    rc = check_launch("moe_prof_hbm_ceiling");
+  } else {
+    const int blocks = prop.multiProcessorCount * 8;
+    auto run = [&]() { hipLaunchKernelGGL(k_hbm_probe, dim3(blocks), dim3(256), 0, nullptr, mode, x, y, n, sink); };
+    for (int w = 0; w < 3; ++w) run();
+    hipEventRecord(e0, nullptr);
+    for (int r = 0; r < 10; ++r) run();
+    hipEventRecord(e1, nullptr);
+    if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+      rc = check_launch("moe_prof_hbm_ceiling");
+  }
+  if (rc == 0) *gbps = moved / ((double)ms / 10.0 * 1e-3) / 1e9;
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  if (x) hipFree(x);
+  if (y) hipFree(y);
+  if (sink) hipFree(sink);
+  return rc;
+}
+
 extern "C" int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, double* clock_mhz) {
   if (iters < 1 || iters > (1 << 24) || !tflops || !clock_mhz)
     return fail_arg("moe_prof_mfma_ceiling: bad arguments (1 <= iters <= 2^24, non-null outputs)");

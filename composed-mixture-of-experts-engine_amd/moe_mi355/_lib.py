@@ -33,6 +33,7 @@ _SIGNATURES = {
     "moe_prof_summary": (_I32, [ctypes.c_char_p, ctypes.POINTER(_I64), ctypes.POINTER(ctypes.c_double)]),
     "moe_prof_kernel_name": (_I32, [_I64, ctypes.c_char_p, _SZ]),
     "moe_prof_mfma_ceiling": (_I32, [_I64, _I32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "moe_prof_hbm_ceiling": (_I32, [_I64, _I32, ctypes.POINTER(ctypes.c_double)]),
     "moe_router_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I32, _I32]),
     "moe_router_fwd_lds_bytes": (_I64, [_I64, _I64, _I64, _I32, _I32]),
     "moe_router_fwd": (
@@ -153,6 +154,14 @@ def prof_mfma_ceiling(iters: int = 100000, fp8: bool = False) -> tuple:
     check(load().moe_prof_mfma_ceiling(int(iters), 1 if fp8 else 0, ctypes.byref(tf), ctypes.byref(mhz)),
           "moe_prof_mfma_ceiling")
     return float(tf.value), float(mhz.value)
+
+
+def prof_hbm_ceiling(nbytes: int, mode: int) -> float:
+    """GB/s moved by a plain stream on the current device: mode 0 read, 1 write, 2 copy, 3 fan-out (each 4 KB row
+    read once, written 6 times)."""
+    g = ctypes.c_double(0.0)
+    check(load().moe_prof_hbm_ceiling(int(nbytes), int(mode), ctypes.byref(g)), "moe_prof_hbm_ceiling")
+    return float(g.value)
 
 
 def dtype_code(dt: torch.dtype) -> int:

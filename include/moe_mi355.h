@@ -73,6 +73,14 @@ int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
  * ticks per 100 MHz s_memrealtime tick).  Allocates and synchronizes. */
 int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, double* clock_mhz);
 
+/* HBM ceiling of the current device (bench only; no counterpart in the
+ * reference): 10 timed grid-stride streams of 16-byte non-temporal accesses
+ * (8 blocks of 256 threads per CU) over fresh buffers: mode 0 reads `bytes`,
+ * 1 writes `bytes`, 2 copies `bytes` (2x moved), 3 reads bytes/4096 rows of
+ * 4 KB once and writes each to 6 rows (7x moved: the permute's shape at K = 6).
+ * Returns the moved bytes per second in GB/s.  Allocates and synchronizes. */
+int moe_prof_hbm_ceiling(int64_t bytes, int mode, double* gbps);
+
 /* ------------------------------------------------------------------------
  * Router forward: logits = x @ wg (+ bias), p = softmax(logits), top-k of p
  * (descending, exact ties -> lower expert index), w = v / max(sum v, 1e-30),
