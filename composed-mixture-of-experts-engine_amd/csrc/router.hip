@@ -1017,7 +1017,9 @@ __device__ __forceinline__ void glogit_token(const float* __restrict__ logits, c
   const float lse = m + __logf(s);
 #pragma unroll
   for (int j = 0; j < EPL; ++j) p[j] *= inv;
-  if (gw != nullptr) {
+  // With K == 1 the renormalised weight is v / v = 1 (the top-1 probability is at least 1/E), so no gradient
+  // reaches the logits through it: the term is skipped rather than formed as a difference of rounded equals.
+  if (gw != nullptr && K > 1) {
     // S = max(sum v, 1e-30); gwv = sum gw*v; grad_v = gw/S - gwv/S^2
     // v_k = p[e_k], picked from this lane's registers (the lane holding e_k contributes, the row sums)
     float S = 0.f, gwv = 0.f;
@@ -1081,7 +1083,7 @@ __device__ __forceinline__ void glogit_token_regs(const float (&lg)[EPL], const 
   const float lse = m + __logf(s);
 #pragma unroll
   for (int j = 0; j < EPL; ++j) p[j] *= inv;
-  if (has_gw) {
+  if (has_gw && K > 1) {  // K == 1: the renormalised weight is identically 1 (see glogit_token)
     float v[KR], S = 0.f, gwv = 0.f;
 #pragma unroll
     for (int k = 0; k < KR; ++k) {

@@ -43,6 +43,10 @@ SHAPES = [
     (50, 72, 8, 2, torch.bfloat16, torch.bfloat16),       # H % 32 != 0 -> generic path
     (333, 256, 24, 20, torch.float32, torch.float32),     # K > 16, generic path
     (200, 64, 8, 2, torch.bfloat16, torch.float32),       # mixed dtypes -> generic path
+    (513, 1024, 8, 5, torch.bfloat16, torch.bfloat16),    # E = 8, K > 4: 16-wave backward, ids read where G is formed
+    (700, 1024, 6, 3, torch.bfloat16, torch.bfloat16),    # E < 8, K = 3: 16-wave backward, per-element gate rows
+    (2048, 2048, 4, 1, torch.bfloat16, torch.bfloat16),   # K = 1, E = 4 on the 16-wave backward
+    (300, 512, 8, 2, torch.bfloat16, torch.bfloat16),     # H % 1024 != 0: 4-wave backward with 8 G slots
 ]
 
 
