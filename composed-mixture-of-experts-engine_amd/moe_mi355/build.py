@@ -1,9 +1,14 @@
-"""Build recipe for libmoe_mi355.so (hipcc, gfx950 only).
+"""Build recipe for libmoe_mi355.so (hipcc, gfx950 only) and its torch binding.
 
 Each ``csrc/*.hip`` file is compiled to an object in ``csrc/_build/`` (in
 parallel) and the objects are linked into ``moe_mi355/libmoe_mi355.so``.  The
 library has no torch dependency: it exports the plain C ABI declared in
 ``include/moe_mi355.h`` and is loaded with ctypes.
+
+``csrc/torch_router.cpp`` (host code only) is then compiled against torch's
+headers into the Python extension ``moe_mi355/_moe_torch.so``: the router's
+autograd Function in C++, calling the same C ABI (it links libmoe_mi355.so
+from its own directory).
 """
 
 from __future__ import annotations
@@ -56,8 +61,41 @@ def _compile(hipcc: str, src: str) -> str:
     return obj
 
 
+TORCH_EXT = os.path.join(PKG_DIR, "_moe_torch.so")
+
+
+def build_torch_binding(hipcc: str) -> str:
+    """Compile csrc/torch_router.cpp into moe_mi355/_moe_torch.so (needs libmoe_mi355.so built first)."""
+    import sysconfig
+
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    src = os.path.join(CSRC, "torch_router.cpp")
+    obj = os.path.join(BUILD, "torch_router.o")
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    incs = ["-I/opt/rocm/include"] + [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}"]
+    cmd = [hipcc, "-x", "c++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", "-DTORCH_EXTENSION_NAME=_moe_torch", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *incs, "-c", src, "-o", obj]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed for {src}:\n{res.stdout}\n{res.stderr}")
+    tmp = TORCH_EXT + ".tmp"
+    libs = [f"-L{p}" for p in ce.library_paths()] + ["-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+                                                      "-ltorch_python"]
+    cmd = [hipcc, "-shared", "-fPIC", obj, f"-L{PKG_DIR}", "-l:libmoe_mi355.so", "-Wl,-rpath,$ORIGIN", *libs,
+           "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed for {TORCH_EXT}:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, TORCH_EXT)
+    return TORCH_EXT
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every csrc/*.hip file and link libmoe_mi355.so; returns its path."""
+    """Compile every csrc/*.hip file and link libmoe_mi355.so, then the torch binding; returns the library's
+    path."""
     hipcc = _hipcc()
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
@@ -72,6 +110,9 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
+    build_torch_binding(hipcc)
+    if verbose:
+        print(f"built {TORCH_EXT}", file=sys.stderr)
     return LIB
 
 

@@ -22,7 +22,7 @@ from typing import Optional
 
 import torch
 
-from . import ops
+from . import _lib as L
 
 STAT_Z = 0
 STAT_AUX = 1
@@ -34,32 +34,44 @@ STAT_NONFINITE = 6
 STAT_DEAD = 7
 
 
-class RouterCore(torch.autograd.Function):
+_native = None
+
+
+def _binding():
+    """The native autograd binding (moe_mi355/_moe_torch.so, built with libmoe_mi355.so)."""
+    global _native
+    if _native is None:
+        try:
+            from . import _moe_torch
+        except ImportError as e:
+            raise RuntimeError(
+                "moe_mi355/_moe_torch.so is not built or does not load; run __graft_entry__.build() "
+                f"(or python moe_mi355/build.py) on a host with ROCm/hipcc ({e})"
+            ) from e
+        _native = _moe_torch
+    return _native
+
+
+class RouterCore:
     """(x [N,H], gate_w [H,E], k, aux_coef, z_coef, bias|None) ->
-    (idx, w, aux, z, logits, cnt, stats)."""
+    (idx, w, aux, z, logits, cnt, stats).
+
+    ``apply`` runs a torch C++ autograd Function (csrc/torch_router.cpp): the forward launches moe_router_fwd
+    and saves (x, gate_w, logits, idx, cnt); the backward, run by the autograd engine without a return to
+    Python, launches moe_router_bwd with the upstream gradients of w, aux and z (an aux or z output that gets
+    no gradient contributes no term).  idx, logits, cnt and stats are not differentiable; no gradient flows
+    to k, the coefficients or the bias.  The checks below raise the errors the ctypes path raises."""
 
     @staticmethod
-    def forward(ctx, x, gate_w, k: int, aux_coef: float, z_coef: float, bias: Optional[torch.Tensor] = None):
-        idx, w, logits, lse, cnt, stats, aux, z = ops.router_forward(
-            x, gate_w, k, bias, aux_coef=aux_coef, z_coef=z_coef, with_losses=True
-        )
-        ctx.save_for_backward(x, gate_w, logits, idx, cnt)
-        ctx.aux_coef = float(aux_coef)
-        ctx.z_coef = float(z_coef)
-        ctx.set_materialize_grads(False)
-        ctx.mark_non_differentiable(idx, logits, cnt, stats)
-        return idx, w, aux, z, logits, cnt, stats
-
-    @staticmethod
-    def backward(ctx, g_idx, g_w, g_aux, g_z, g_logits, g_cnt, g_stats):
-        x, gate_w, logits, idx, cnt = ctx.saved_tensors
-        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        if not (need_x or need_w):
-            return None, None, None, None, None, None
-        aux_coef = ctx.aux_coef if g_aux is not None else 0.0
-        z_coef = ctx.z_coef if g_z is not None else 0.0
-        dx, dw = ops.router_backward(x, gate_w, logits, idx, g_w, cnt, g_aux, g_z, aux_coef, z_coef)
-        return (dx if need_x else None), (dw if need_w else None), None, None, None, None
+    def apply(x, gate_w, k: int, aux_coef: float, z_coef: float, bias: Optional[torch.Tensor] = None):
+        L.require_device(x, gate_w, bias)
+        N, H = x.shape
+        H2, E = gate_w.shape
+        if H != H2:
+            raise ValueError(f"router_forward: hidden dims differ ({H} vs {H2})")
+        L.dtype_code(x.dtype)
+        L.dtype_code(gate_w.dtype)
+        return tuple(_binding().router_core(x, gate_w, int(k), float(aux_coef), float(z_coef), bias))
 
 
 def route(x: torch.Tensor, gate_w: torch.Tensor, k: int, aux_coef: float = 0.0, z_coef: float = 0.0,

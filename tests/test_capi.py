@@ -86,3 +86,20 @@ def test_cpu_tensors_are_rejected_not_routed_to_a_fallback():
 
     with pytest.raises(RuntimeError, match="GPU"):
         ops.router_forward(torch.zeros(4, 8), torch.zeros(8, 4), 2)
+
+
+def test_torch_binding_loads_and_shares_the_library():
+    """moe_mi355/_moe_torch.so (the router's C++ autograd Function) imports, links the in-tree
+    libmoe_mi355.so, and its entry point rejects CPU tensors through RouterCore's checks."""
+    import torch
+
+    from moe_mi355 import router as R
+
+    mod = R._binding()
+    assert os.path.dirname(os.path.abspath(mod.__file__)) == os.path.dirname(os.path.abspath(_lib.LIB_PATH))
+    assert callable(mod.router_core)
+    with open("/proc/self/maps") as f:
+        maps = f.read()
+    assert os.path.realpath(_lib.LIB_PATH) in maps
+    with pytest.raises(RuntimeError, match="AMD Instinct GPU"):
+        R.RouterCore.apply(torch.zeros(4, 8), torch.zeros(8, 2), 1, 0.0, 0.0, None)
