@@ -831,7 +831,7 @@ def main():
     out = {
         "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8-e4m3" if args.workload == "fp8_fwd" else "bf16",
+        "dtype": {"fp8_fwd": "fp8-e4m3", "c1": "f32"}.get(args.workload, "bf16"),
         "data": "synthetic (seeded randn of the BASELINE config shapes; random-init weights)", "config": config,
         "roofline": roof, "cpu_baseline": cpu,
     }

@@ -816,6 +816,119 @@ __global__ __launch_bounds__(512) void k_router_fwd_wide(
 }
 
 // ---------------------------------------------------------------------------
+// Forward, fp32 x and fp32 gate (E <= 64, H % 4 == 0, x 16-byte aligned).  The gate GEMM runs on
+// v_mfma_f32_16x16x4_f32 (fp32 products, fp32 sums), whose 16x16 accumulator layout is the one the bf16
+// kernels route from.  Block = 8 waves = TG groups of 16 tokens x HS = 8 / TG waves per group; wave hp of a
+// group sums its logits over the hp-th contiguous 1/HS of the 16-column chunks of the hidden dim.  Per chunk
+// c, lane l reads x[t0 + l % 16][k .. k + 3] with one 16-byte load (k = 16 c + 4 (l / 16)) and feeds the four
+// values to four MFMAs together with the gate rows k .. k + 3 of its expert column l % 16: in MFMA s, the
+// k slot l / 16 holds k + s for A and for B alike, which is all the product needs.  The HS partial tiles are
+// summed in LDS in wave order, wave hp = 0 of each group routes it (route_group), and the block tail
+// publishes the block's statistics and folds every block's in the last block to finish.
+// ---------------------------------------------------------------------------
+template <int NT, int TG>
+__global__ __launch_bounds__(512) void k_router_fwd_f32(
+    const float* __restrict__ x, const float* __restrict__ wg, const float* __restrict__ bias, int N, int H, int E,
+    int K, int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt, float* __restrict__ logits_out,
+    float* __restrict__ lse_out, int* __restrict__ part_cnt, float* __restrict__ part_p, float* __restrict__ part_z,
+    unsigned* __restrict__ ticket, float aux_coef, float z_coef, int64_t* __restrict__ cnt_out,
+    float* __restrict__ stats, float* __restrict__ aux_out, float* __restrict__ z_out) {
+  constexpr int HS = 8 / TG;
+  constexpr int U = 4;  // chunks per load group
+  __shared__ f32x4 s_acc[(HS > 1 ? HS - 1 : 1) * TG * NT * 64];
+  __shared__ int s_cnt[NT * 16];
+  __shared__ float s_p[TG][NT * 16];
+  __shared__ float s_z[TG];
+  __shared__ int s_nf[TG];
+  __shared__ int s_last;
+  __shared__ float s_fin[finalize_scratch_floats<512>()];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int tg = wv / HS;
+  const int hp = wv % HS;
+  const int n = lane & 15;
+  const int q = lane >> 4;
+  const int t0 = blockIdx.x * (16 * TG) + tg * 16;
+  for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
+
+  const int row = min(t0 + n, N - 1);
+  const float* xr = x + (int64_t)row * H + 4 * q;
+  const int nc = (H + 15) / 16;   // chunks; all but a last partial one (H % 16 != 0) lie inside the row
+  const int nfull = H / 16;
+  const int per = (nc + HS - 1) / HS;
+  const int c_beg = min(nc, hp * per);
+  const int c_end = min(nc, c_beg + per);
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // gate row k + s of expert column nt * 16 + n (zero past E or past H)
+  auto gate = [&](int k, int s, int nt) -> float {
+    const int e = nt * 16 + n;
+    return (e < E && k + s < H) ? wg[(int64_t)(k + s) * E + e] : 0.f;
+  };
+  auto chunk_mma = [&](const f32x4& a, const float (&b)[NT][4]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s2], b[nt][s2], acc[nt], 0, 0, 0);
+  };
+  if (t0 < N) {
+    const int c_mid = min(c_end, nfull);
+    int c = c_beg;
+    for (; c + U <= c_mid; c += U) {
+      f32x4 a[U];
+      float b[U][NT][4];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        a[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + (c + u) * 16));
+        const int k = (c + u) * 16 + 4 * q;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) b[u][nt][s2] = gate(k, s2, nt);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) chunk_mma(a[u], b[u]);
+    }
+    for (; c < c_end; ++c) {  // the rest, and the last partial chunk (lanes past H read zeros)
+      const int k = c * 16 + 4 * q;
+      const f32x4 a = k < H ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr + c * 16))
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+      float b[NT][4];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) b[nt][s2] = gate(k, s2, nt);
+      chunk_mma(a, b);
+    }
+  }
+
+  if constexpr (HS > 1) {
+    if (hp > 0) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) s_acc[(((hp - 1) * TG + tg) * NT + nt) * 64 + lane] = acc[nt];
+    }
+  }
+  __syncthreads();  // s_cnt zeroed, partial tiles visible
+  if constexpr (HS > 1) {
+    if (hp == 0) {
+#pragma unroll
+      for (int q2 = 1; q2 < HS; ++q2)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[nt] += s_acc[(((q2 - 1) * TG + tg) * NT + nt) * 64 + lane];
+    }
+  }
+  if (hp == 0) route_group<NT>(acc, t0, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt, s_p[tg],
+                              &s_z[tg], &s_nf[tg]);
+  __syncthreads();
+  fwd_block_tail<TG, NT>(s_cnt, s_p, s_z, s_nf, s_last, s_fin, N, E, K, part_cnt, part_p, part_z, ticket, aux_coef,
+                         z_coef, cnt_out, stats, aux_out, z_out);
+}
+
+// ---------------------------------------------------------------------------
 // Generic forward: logits by VALU (one wave per token), then route_from_logits.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_logits_generic(const void* __restrict__ x, int x_dt,
@@ -1740,6 +1853,80 @@ __global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __rest
       }
 }
 
+// Backward, fp32 x and gate (E <= 16, H % 4 == 0, x and dx 16-byte aligned): dx = G wg^T and the per-chunk
+// partials of dwg = x^T G in one pass over x.  Block = 4 waves on one 256-column slice of the hidden dim
+// (blockIdx.x) and one chunk of tc_len tokens (blockIdx.y); lane l owns columns h = h0 + 4 l .. h + 3 and keeps
+// their gate rows in registers.  Wave w takes the chunk's tokens w, w + 4, ...: per token it reads the row G[t]
+// (wave-uniform), its 4 x values (one 16-byte load), stores its 4 dx values (one 16-byte store: each a sum
+// over e = 0 .. E-1 in order) and adds x * G into its 4 x EL dwg sums.  The 4 waves' sums are added in wave
+// order through LDS and stored as the chunk's partial ws_dw[chunk][h * E + e] (the fixed-order reduce over
+// chunks follows).
+template <int EL>
+__global__ __launch_bounds__(256) void k_router_dxdw_f32(const float* __restrict__ x, const float* __restrict__ wg,
+                                                         const float* __restrict__ G, int N, int H, int E,
+                                                         int tc_len, float* __restrict__ dx,
+                                                         float* __restrict__ ws_dw) {
+  __shared__ float s_part[3][4 * EL][65];  // waves 1-3's sums, [wave][i * EL + e][lane] (padded rows)
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = blockIdx.x * 256 + 4 * lane;
+  const bool hv = h < H;
+  const int tbeg = blockIdx.y * tc_len;
+  const int tend = min(N, tbeg + tc_len);
+  float gr[4][EL];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < EL; ++e) gr[i][e] = (hv && e < E) ? wg[(int64_t)(h + i) * E + e] : 0.f;
+  float acc[4][EL];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < EL; ++e) acc[i][e] = 0.f;
+#pragma unroll 2
+  for (int t = tbeg + wv; t < tend; t += 4) {
+    float g[EL];
+#pragma unroll
+    for (int e = 0; e < EL; ++e) g[e] = e < E ? G[(int64_t)t * E + e] : 0.f;
+    const f32x4 xv = hv ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + (int64_t)t * H + h))
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < EL; ++e) v = fmaf(g[e], gr[i][e], v);
+      o[i] = v;
+    }
+    if (hv) __builtin_nontemporal_store(o, reinterpret_cast<f32x4*>(dx + (int64_t)t * H + h));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < EL; ++e) acc[i][e] = fmaf(xv[i], g[e], acc[i][e]);
+  }
+  if (wv > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < EL; ++e) s_part[wv - 1][i * EL + e][lane] = acc[i][e];
+  }
+  __syncthreads();
+  if (wv == 0 && hv) {
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < EL; ++e) acc[i][e] += s_part[w][i * EL + e][lane];
+    float* dst = ws_dw + (int64_t)blockIdx.y * H * E + (int64_t)h * E;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < EL; ++e)
+        if (e < E) dst[i * E + e] = acc[i][e];
+  }
+}
+
 // Generic dx = G wg^T: one thread per (t, h).
 __global__ __launch_bounds__(256) void k_router_dx_generic(const float* __restrict__ G, const void* __restrict__ wg,
                                                            int w_dt, int N, int H, int E, void* __restrict__ dx,
@@ -1836,6 +2023,7 @@ constexpr int fwd_u(int NT) { return NT <= 4 ? 4 : 2; }
 int fwd_tokens_per_block(int NT) { return 16 * (4 / fwd_hs(NT)); }
 
 struct FwdPlan {
+  bool f32;     // k_router_fwd_f32 (fp32 x and gate, E <= 64, H % 4 == 0)
   bool mfma;
   bool stream;  // k_router_fwd_stream (E <= 32, H % 256 == 0)
   bool wide;    // k_router_fwd_wide (32 < E <= 256, H % 64 == 0)
@@ -1854,7 +2042,13 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt, bool allow
   if (p.NT > 4 && p.NT < 8) p.NT = 8;
   p.stream = allow_stream && p.mfma && E <= 32 && H % 256 == 0;
   p.wide = allow_stream && x_dt == MOE_BF16 && w_dt == MOE_BF16 && E > 32 && E <= kMaxE && H % 64 == 0;
-  if (p.wide) {
+  p.f32 = allow_stream && x_dt == MOE_F32 && w_dt == MOE_F32 && E <= 64 && H % 4 == 0;
+  if (p.f32) {
+    // 16 * TG tokens per block: the largest TG that still gives about one block per CU (256)
+    const int64_t groups = cdiv(N, 16);
+    p.TG = groups >= 256 * 8 ? 8 : (groups >= 256 * 4 ? 4 : (groups >= 256 * 2 ? 2 : 1));
+    p.nblk = cdiv(N, 16 * p.TG);
+  } else if (p.wide) {
     p.mfma = true;
     p.NT = E <= 64 ? 4 : (E <= 128 ? 8 : 16);
     p.nblk = cdiv(N, WideFwd<4>::ROWS);
@@ -1885,6 +2079,7 @@ FwdPlan plan_fwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt, bool allow
 }
 
 struct BwdPlan {
+  bool f32;     // k_router_glogits + k_router_dxdw_f32 (fp32 x and gate, E <= 16, H % 4 == 0)
   bool mfma;
   bool stream;  // k_router_dxdw_stream (E <= 32, H % 256 == 0)
   bool wide;    // k_router_glogits + k_router_dxdw_wide (32 < E <= 128, H % 256 == 0)
@@ -1903,7 +2098,15 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
   if (p.NTE > 4 && p.NTE < 8) p.NTE = 8;
   p.stream = p.mfma && E <= 32 && H % 256 == 0;
   p.wide = p.mfma && E > 32 && H % 256 == 0;
-  if (p.wide) {
+  p.f32 = x_dt == MOE_F32 && w_dt == MOE_F32 && E <= 16 && H % 4 == 0;
+  if (p.f32) {
+    // about 1024 blocks of (256-column slice, token chunk), at most 8 tokens per wave before the chunks grow
+    const int64_t nht = cdiv(H, 256);
+    const int64_t want = std::max<int64_t>(1, 1024 / nht);
+    p.nchunk = (int)std::max<int64_t>(1, std::min<int64_t>(want, cdiv(N, 32)));
+    p.tc_len = (int)cdiv(N, p.nchunk);
+    p.nchunk = (int)cdiv(N, p.tc_len);
+  } else if (p.wide) {
     // about one block per CU; long chunks keep the fp32 dwg partials few
     const int nht = (int)(H / 256);
     const int want = std::max(1, kWideBwdBlocks / nht);
@@ -2043,7 +2246,11 @@ extern "C" int64_t moe_router_fwd_lds_bytes(int64_t N, int64_t H, int64_t E, int
   if (N <= 0 || H <= 0 || E < 1 || E > kMaxE) return 0;
   const FwdPlan p = plan_fwd(N, H, E, x_dtype, wg_dtype);
   const void* f = nullptr;
-  if (p.wide) {
+  if (p.f32) {
+    // the MFMA form when x is 16-byte aligned (the usual case); all TG variants share their LDS layout per NT
+    f = p.NT == 1 ? (const void*)k_router_fwd_f32<1, 1> : p.NT == 2 ? (const void*)k_router_fwd_f32<2, 1>
+                                                                     : (const void*)k_router_fwd_f32<4, 1>;
+  } else if (p.wide) {
     f = p.NT == 4 ? (const void*)k_router_fwd_wide<4> : p.NT == 8 ? (const void*)k_router_fwd_wide<8>
                                                                  : (const void*)k_router_fwd_wide<16>;
   } else if (p.stream) {
@@ -2093,6 +2300,29 @@ extern "C" int moe_router_fwd(const void* x, int x_dtype, const void* wg, int wg
   int* pc = reinterpret_cast<int*>(ws + p.off_cnt);
   float* pp = reinterpret_cast<float*>(ws + p.off_p);
   float* pz = reinterpret_cast<float*>(ws + p.off_z);
+  if (p.f32 && aligned16(x)) {
+    // fp32 form: MFMA gate GEMM, routing and the statistics fold in one launch (ticket zero on entry and exit)
+    unsigned* ticket = reinterpret_cast<unsigned*>(ws + p.off_ticket);
+    const float* xf = static_cast<const float*>(x);
+    const float* wf = static_cast<const float*>(wg);
+#define MOE_FWDF(NTv, TGv)                                                                                         \
+  MOE_LAUNCH("k_router_fwd_f32", (k_router_fwd_f32<NTv, TGv>), dim3(p.nblk), dim3(512), 0, s, xf, wf, bias, (int)N,   \
+             (int)H, (int)E, (int)K, idx_out, w_out, w_dtype, logits_out, lse_out, pc, pp, pz, ticket, aux_coef,    \
+             z_coef, cnt_out, stats_out, aux_out, z_out)
+#define MOE_FWDF_TG(NTv)          \
+  do {                            \
+    if (p.TG == 8) MOE_FWDF(NTv, 8); \
+    else if (p.TG == 4) MOE_FWDF(NTv, 4); \
+    else if (p.TG == 2) MOE_FWDF(NTv, 2); \
+    else MOE_FWDF(NTv, 1);        \
+  } while (0)
+    if (p.NT == 1) MOE_FWDF_TG(1);
+    else if (p.NT == 2) MOE_FWDF_TG(2);
+    else MOE_FWDF_TG(4);
+#undef MOE_FWDF_TG
+#undef MOE_FWDF
+    return check_launch("k_router_fwd_f32");
+  }
   const bool mfma = p.mfma && aligned16(x);
   if (mfma && p.stream) {
     // streaming form: raw gate, finalize folded into the last block (ticket zero on entry and on exit)
@@ -2280,6 +2510,18 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
     else return fail_arg("moe_router_bwd: internal tile error");
 #undef MOE_DXDW
     if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+  } else if (p.f32 && aligned16(x) && aligned16(dx_out)) {
+    const dim3 grid((unsigned)cdiv(H, 256), (unsigned)p.nchunk);
+    const float* xf = static_cast<const float*>(x);
+    const float* wf = static_cast<const float*>(wg);
+    float* dxf = static_cast<float*>(dx_out);
+    if (E <= 8)
+      MOE_LAUNCH("k_router_dxdw_f32", k_router_dxdw_f32<8>, grid, dim3(256), 0, s, xf, wf, G, (int)N, (int)H, (int)E,
+                 p.tc_len, dxf, wsdw);
+    else
+      MOE_LAUNCH("k_router_dxdw_f32", k_router_dxdw_f32<16>, grid, dim3(256), 0, s, xf, wf, G, (int)N, (int)H, (int)E,
+                 p.tc_len, dxf, wsdw);
+    if (int rc = check_launch("k_router_dxdw_f32")) return rc;
   } else {
     const int64_t NH = N * H;
     MOE_LAUNCH("k_router_dx_generic", k_router_dx_generic, dim3((unsigned)std::min<int64_t>(16384, (NH + 255) / 256)), dim3(256), 0,

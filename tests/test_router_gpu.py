@@ -24,7 +24,12 @@ pytestmark = pytest.mark.gpu
 
 # (N, H, E, K, x dtype, gate dtype)
 SHAPES = [
-    (4096, 512, 8, 2, torch.float32, torch.float32),      # C1 (generic kernels)
+    (4096, 512, 8, 2, torch.float32, torch.float32),      # C1 (fp32 MFMA forward, fp32 dx / dwg kernel)
+    (1000, 300, 16, 4, torch.float32, torch.float32),     # fp32: H % 16 != 0 (partial last chunk), E = 16
+    (20000, 256, 64, 6, torch.float32, torch.float32),    # fp32: 4 expert tiles, 4 groups per block
+    (40000, 128, 8, 2, torch.float32, torch.float32),     # fp32: 8 groups per block
+    (257, 64, 3, 2, torch.float32, torch.float32),        # fp32: E < 16, more waves than chunks
+    (130, 70, 8, 2, torch.float32, torch.float32),        # fp32 with H % 4 != 0 -> generic kernels
     (16384, 4096, 8, 2, torch.bfloat16, torch.bfloat16),  # C2 at full size (MFMA kernels)
     (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),   # ragged token count
     (64, 64, 8, 8, torch.bfloat16, torch.bfloat16),       # K == E
@@ -41,7 +46,7 @@ SHAPES = [
     (100, 96, 10, 3, torch.bfloat16, torch.bfloat16),     # E not a multiple of 16
     (128, 256, 40, 18, torch.bfloat16, torch.bfloat16),   # K > 16 on the MFMA path
     (50, 72, 8, 2, torch.bfloat16, torch.bfloat16),       # H % 32 != 0 -> generic path
-    (333, 256, 24, 20, torch.float32, torch.float32),     # K > 16, generic path
+    (333, 256, 24, 20, torch.float32, torch.float32),     # K > 16; fp32 forward, generic backward (E > 16)
     (200, 64, 8, 2, torch.bfloat16, torch.float32),       # mixed dtypes -> generic path
     (513, 1024, 8, 5, torch.bfloat16, torch.bfloat16),    # E = 8, K > 4: 16-wave backward, ids read where G is formed
     (700, 1024, 6, 3, torch.bfloat16, torch.bfloat16),    # E < 8, K = 3: 16-wave backward, per-element gate rows
@@ -203,7 +208,8 @@ def test_router_forward_workspace_reuse_across_paths():
         (300, 2048, 64, 6, torch.bfloat16, torch.bfloat16),   # wide streaming, 3 blocks
         (96, 96, 64, 4, torch.bfloat16, torch.bfloat16),      # packed-gate kernel + finalize launch
         (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),   # streaming, other block count
-        (4096, 512, 8, 2, torch.float32, torch.float32),      # generic path
+        (4096, 512, 8, 2, torch.float32, torch.float32),      # fp32 MFMA form, its own fold
+        (130, 70, 8, 2, torch.float32, torch.float32),        # generic path
         (37, 512, 32, 1, torch.bfloat16, torch.bfloat16),     # streaming, a single block
     ]
     for rep in range(2):
@@ -211,3 +217,33 @@ def test_router_forward_workspace_reuse_across_paths():
             N, H, E, K, xd, wd = shape
             x, w, _ = _inputs(N, H, E, K, xd, wd, seed=100 + 7 * i + rep)
             _check_forward(x, w, K)
+
+
+@pytest.mark.parametrize("losses", [False, True], ids=["plain", "aux_z"])
+def test_router_fp32_unaligned_x_takes_the_generic_kernels(losses):
+    """fp32 x whose data starts 4 bytes past a 16-byte boundary (a contiguous view one element into its storage):
+    the fp32 MFMA forward and the fp32 dx / dwg kernel read x with 16-byte loads, so the call takes the generic
+    kernels under the same workspace plan; forward and backward still match the oracle."""
+    N, H, E, K = 1000, 512, 8, 2
+    say(f"[router fp32 unaligned] losses={losses}")
+    x, w, gw = _inputs(N, H, E, K, torch.float32, torch.float32, seed=77)
+    d = dev()
+    base = torch.empty(N * H + 1, device=d)
+    xv = base[1:].view(N, H)
+    with torch.no_grad():
+        xv.copy_(x.to(d))
+    assert xv.data_ptr() % 16 != 0 and xv.is_contiguous()
+    xv.requires_grad_(True)
+    wd_ = w.to(d).requires_grad_(True)
+    alpha, beta = (0.01, 1e-3) if losses else (0.0, 0.0)
+    idx, wt, aux, z, logits, cnt, stats = RouterCore.apply(xv, wd_, K, alpha, beta, None)
+    loss = (wt * gw.to(d)).sum() + (aux + z if losses else 0.0)
+    loss.backward()
+    torch.cuda.synchronize()
+    fwd = OR.route_fwd(x, w, K)
+    ok = fwd["margin"] > MARGIN
+    assert torch.equal(idx.cpu()[ok], fwd["idx"][ok])
+    assert_rel(logits, fwd["logits"], 1e-5, "logits")
+    ref = OR.router_full(x, w, K, grad_w=gw, alpha=alpha, beta=beta, idx_override=idx.cpu())
+    assert_rel(xv.grad, ref["dX"], 1e-5, "dX", floor=1e-4)
+    assert_rel(wd_.grad, ref["dW"], 1e-5, "dW", floor=1e-4)
