@@ -35,6 +35,7 @@ the fused HIP grouped GEMM; other dtypes call the expert modules per expert.
 
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import List, Optional
 
@@ -259,8 +260,22 @@ class DistributedMoELayer(nn.Module):
             raise ValueError(f"tokens must be rank 2 or 3, got {tokens.dim()}")
         H = tokens.shape[-1]
         flat = tokens.reshape(-1, H)
-        idx, weights, _cnt = self.router(flat)
+        with self._deferred_router_check():
+            idx, weights, _cnt = self.router(flat)
         return self._experts_forward(flat, idx, weights).reshape(original_shape)
+
+    @contextlib.contextmanager
+    def _deferred_router_check(self):
+        """With ``check_numerics`` the router's checks (token conservation, non-finite logits) run at the end
+        of the forward, at the synchronisation of the output NaN check, rather than right after the routing:
+        the expert path is enqueued first, so the GPU does not wait for the host in the middle of the forward.
+        The assertions and their order are the reference's (router first, then the output)."""
+        r = self.router
+        r._defer_check = self.check_numerics and r.sync_profile
+        try:
+            yield
+        finally:
+            r._defer_check = False
 
     def forward_normed(self, tokens: torch.Tensor, norm_weight: torch.Tensor, eps: float) -> torch.Tensor:
         """``forward(rmsnorm(tokens))`` with the norm fused into the router's read of the hidden state
@@ -270,7 +285,8 @@ class DistributedMoELayer(nn.Module):
             raise ValueError(f"tokens must be rank 2 or 3, got {tokens.dim()}")
         H = tokens.shape[-1]
         flat = tokens.reshape(-1, H)
-        xn, idx, weights, _cnt = self.router.forward_with_norm(flat, norm_weight, eps)
+        with self._deferred_router_check():
+            xn, idx, weights, _cnt = self.router.forward_with_norm(flat, norm_weight, eps)
         return self._experts_forward(xn, idx, weights).reshape(original_shape)
 
     def _experts_forward(self, flat: torch.Tensor, idx: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
@@ -290,7 +306,9 @@ class DistributedMoELayer(nn.Module):
             out = self._forward_per_expert(flat, weights, p, timer)
         self._expert_timer = timer
         if self.check_numerics:
-            assert not torch.isnan(out).any(), (
+            has_nan = torch.isnan(out).any()  # enqueued before the router's deferred checks synchronise
+            self.router.check_pending()
+            assert not has_nan, (
                 "NaN detected in DistributedMoELayer output after combine step. "
                 "Check expert FFN numerics and router weights."
             )

@@ -237,6 +237,9 @@ class MoERouter(torch.nn.Module):
         self.sync_profile = sync_profile
         self._profile: Optional[RouterProfile] = None
         self._pending = None  # what a not-yet-read profile is built from
+        # set by a caller that enqueues more GPU work after the routing and runs the checks itself at its next
+        # synchronisation (check_pending): the forward then does not stop the stream mid-way
+        self._defer_check = False
         self._last_logits: Optional[torch.Tensor] = None
         self.last_aux_loss: Optional[torch.Tensor] = None
         self.last_z_loss: Optional[torch.Tensor] = None
@@ -319,9 +322,15 @@ class MoERouter(torch.nn.Module):
         self._profile = None
         self._pending = (N, _fwd_lds_bytes(flat, self.gate_w), router_fwd_bytes(flat, self.gate_w, self.top_k,
                                                                                    w.dtype), stats, z_plain, timing)
-        if self.sync_profile:
+        if self.sync_profile and not self._defer_check:
             self._resolve(check=True)
         return idx, w, cnt
+
+    def check_pending(self) -> None:
+        """Run the checks of a forward made with the checks deferred (the token conservation and non-finite
+        logits asserts; one device-to-host copy, which waits for the work enqueued so far)."""
+        if self._pending is not None:
+            self._resolve(check=True)
 
     def _resolve(self, check: bool = False) -> None:
         """Build ``last_profile`` from the pending forward: one device-to-host copy of the statistics (after

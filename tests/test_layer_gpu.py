@@ -156,3 +156,32 @@ def test_layer_c4_shape_vs_torch_fp32():
     assert_rel(layer.w_gate.grad, wgf.grad, 2e-2, "C4 dw_gate")
     assert_rel(layer.w_up.grad, wuf.grad, 2e-2, "C4 dw_up")
     assert_rel(layer.w_down.grad, wdf.grad, 2e-2, "C4 dw_down")
+
+
+def test_layer_checks_run_at_the_end_of_the_forward():
+    """With check_numerics the router's checks are deferred to the forward's final synchronisation: after
+    the forward nothing is pending, the profile is resolved and the layer's outputs match a forward with
+    the checks off; a non-finite gate still raises the router's assertion (before the output NaN check)
+    from the layer's forward, and the router alone still checks at once."""
+    say("[layer deferred checks]")
+    H, Fd, E, K, N = 256, 512, 8, 2, 300
+    layer = _layer(H, Fd, E, K, torch.bfloat16, layout="routed")
+    assert layer.check_numerics and layer.router.sync_profile
+    x = torch.randn(N, H, device=dev()).to(torch.bfloat16)
+    out = layer(x)
+    assert layer.router._pending is None and not layer.router._defer_check
+    prof = layer.router.last_profile
+    assert prof is not None and prof.kernel_ms > 0.0
+    from moe_mi355.router import STAT_CNT_TOTAL
+    assert int(round(float(layer.router.last_stats_host[STAT_CNT_TOTAL]))) == N * K
+    layer.check_numerics = False
+    out2 = layer(x)
+    assert torch.equal(out, out2)
+    layer.check_numerics = True
+    with torch.no_grad():
+        layer.router.gate_w[0, 3] = float("nan")
+    with pytest.raises(AssertionError, match="NaN in expert indices"):
+        layer(x)
+    assert not layer.router._defer_check
+    with pytest.raises(AssertionError, match="NaN in expert indices"):
+        layer.router(x)
