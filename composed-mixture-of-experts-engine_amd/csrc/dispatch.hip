@@ -31,6 +31,7 @@ namespace moe {
 
 enum PlanMode { kCapacity = 0, kRefSort = 1, kRouted = 2 };
 constexpr int kPlanIB = 2048;  // items per planner block
+constexpr int kPlanMaxK = 128;  // largest top-k of the fused capacity + routed path
 
 // Expert ids are clamped into [0, E) so a malformed index can never address
 // outside the planner's tables (the router only produces ids in range).
@@ -179,6 +180,26 @@ __device__ __forceinline__ void group_rank(const WaveKeys& wk, int w, int lane, 
       else if (key == -1) skip(i);
       // the running count moves on only after every lane of the key group has read it (a wave's LDS
       // operations complete in order)
+      if (valid && (m & lt) == 0) cnt[w * nkeys + key] = run + __popcll(m);
+    }
+  }
+}
+
+// pass 2 of a grouping whose items then take part in a second grouping of the same parts: wk.key[c] <-
+// rekey(i, key, rank) for each item with a key (items without one keep theirs)
+template <class Rekey>
+__device__ __forceinline__ void group_rank_rekey(WaveKeys& wk, int w, int lane, int nkeys, int nbits, int* cnt,
+                                                 Rekey rekey) {
+  const uint64_t lt = lane ? ((~0ull) >> (64 - lane)) : 0ull;
+#pragma unroll
+  for (int c = 0; c < kPlanCh; ++c) {
+    if (c < wk.nch) {  // wave-uniform
+      const int key = wk.key[c];
+      const int64_t i = wk.lo + 64 * c + lane;
+      const bool valid = key >= 0;
+      const uint64_t m = key_match(valid, key, nbits);
+      const int run = valid ? cnt[w * nkeys + key] : 0;
+      if (valid) wk.key[c] = rekey(i, key, run + __popcll(m & lt));
       if (valid && (m & lt) == 0) cnt[w * nkeys + key] = run + __popcll(m);
     }
   }
@@ -605,6 +626,173 @@ __global__ __launch_bounds__(kPlanNT) void k_plan_rank(int mode, PlanKeys pk, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused multi-block path for capacity drops with the routed layout: count -> scan2 -> rank2 (three launches
+// instead of the two groupings' five).  Within one capacity key (column k, expert e) the items of block b take
+// the consecutive capacity ranks base[key][b] + 0, 1, ..., so the block keeps exactly
+// clamp(capacity - base[key][b], 0, count[key][b]) of them: the routed grouping's block counts follow from the
+// capacity scan without a rank pass, and one rank pass does both in-block groupings.
+// ---------------------------------------------------------------------------
+// Scan2: one wave per expert e.  For each block chunk of 256 blocks it loads the block counts of all K keys
+// (k, e) (eight keys per round of loads), writes the capacity bases base[key][b] (exclusive prefix over blocks,
+// carried across chunks in LDS), sums the kept slots per block over the K keys and writes their exclusive
+// prefix over blocks, base_r[e][b]; tot_r[e] = the expert's kept slots.
+__global__ __launch_bounds__(256) void k_plan_scan2(const int* __restrict__ counts, int nblk, int K, int E,
+                                                    int64_t capacity, int* __restrict__ base, int* __restrict__ base_r,
+                                                    int* __restrict__ tot_r) {
+  __shared__ int s_run[4][kPlanMaxK];  // per wave: the running capacity base of each key (k, e)
+  const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;
+  const int e = blockIdx.x * 4 + wq;
+  if (e >= E) return;  // wave-uniform; no block barrier below
+  for (int k = lane; k < K; k += 64) s_run[wq][k] = 0;
+  int run_r = 0;
+  for (int b0 = 0; b0 < nblk; b0 += 256) {
+    int kept[4] = {0, 0, 0, 0};
+    for (int k0 = 0; k0 < K; k0 += 8) {
+      int v[8][4];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int b = b0 + 64 * j + lane;
+          v[kk][j] = (k0 + kk < K && b < nblk) ? counts[(int64_t)((k0 + kk) * E + e) * nblk + b] : 0;
+        }
+      // the 32 wave scans of this round are independent of each other (the carries are added after)
+      int incl[8][4];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) incl[kk][j] = v[kk][j];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1)
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int t = __shfl_up(incl[kk][j], o);
+            if (lane >= o) incl[kk][j] += t;
+          }
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        if (k0 + kk < K) {  // wave-uniform
+          const int key = (k0 + kk) * E + e;
+          int run = s_run[wq][k0 + kk];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int b = b0 + 64 * j + lane;
+            const int bc = run + incl[kk][j] - v[kk][j];
+            if (b < nblk) base[(int64_t)key * nblk + b] = bc;
+            kept[j] += (int)min((int64_t)v[kk][j], max((int64_t)0, capacity - (int64_t)bc));
+            run += __shfl(incl[kk][j], 63);
+          }
+          if (lane == 0) s_run[wq][k0 + kk] = run;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int incl = kept[j];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+      }
+      const int b = b0 + 64 * j + lane;
+      if (b < nblk) base_r[(int64_t)e * nblk + b] = run_r + incl - kept[j];
+      run_r += __shfl(incl, 63);
+    }
+  }
+  if (lane == 0) tot_r[e] = run_r;
+}
+
+// Rank2: one 1024-thread block per kPlanIB slots.  The capacity grouping (keys k*E + e, block bases from scan2)
+// gives each slot its capacity rank and so its drop flag and its key in the routed grouping (its expert, or none
+// for a dropped slot: kept in registers when both groupings split the items over the same waves, else read back
+// from the drop flags, which a block barrier makes visible to the block); a routed row is the expert's offset
+// (exclusive prefix of tot_r) plus the expert's kept slots in earlier blocks plus the in-block rank.  Block 0
+// writes the offsets; rows past the kept ones get -1.
+// LDS: ccnt [cnw * K*E] + kb [K*E] + cnt [nwr * E] + kbr [E + 1] + part [1024] + red [16] ints.
+__global__ __launch_bounds__(kPlanNT) void k_plan_rank2(PlanKeys pk, int64_t M, int nblk, const int* __restrict__ base,
+                                                        const int* __restrict__ base_r, const int* __restrict__ tot_r,
+                                                        int64_t capacity, uint8_t* __restrict__ drop,
+                                                        int* __restrict__ row_slot, int* __restrict__ slot_row,
+                                                        int* __restrict__ offsets, int* __restrict__ ndrop) {
+  extern __shared__ int lds[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = pk.K, E = pk.E;
+  const int cnk = K * E, cnw = plan_nwr(cnk), cnb = nbits_of(cnk);
+  const int nwr = plan_nwr(E), nbits = nbits_of(E);
+  int* ccnt = lds;
+  int* kb = ccnt + cnw * cnk;
+  int* cnt = kb + cnk;
+  int* kbr = cnt + nwr * E;
+  int* part = kbr + E + 1;
+  int* red = part + kPlanNT;
+  const int b = blockIdx.x;
+  const int64_t beg = (int64_t)b * kPlanIB, end = min(M, beg + kPlanIB);
+  WaveKeys wk;
+  if (w < cnw) load_keys(wk, beg, end, cnw, w, lane, pk, kCapacity);
+  int bv[kPlanKPT];
+#pragma unroll
+  for (int j = 0; j < kPlanKPT; ++j) bv[j] = base[(int64_t)min((int)threadIdx.x + j * kPlanNT, cnk - 1) * nblk + b];
+  for (int q = threadIdx.x; q < cnw * cnk; q += kPlanNT) ccnt[q] = 0;
+  for (int q = threadIdx.x; q < nwr * E; q += kPlanNT) cnt[q] = 0;
+  block_excl_scan(tot_r, E, kbr, part);  // kbr = expert offsets; ends with a barrier
+#pragma unroll
+  for (int j = 0; j < kPlanKPT; ++j) {
+    const int key = threadIdx.x + j * kPlanNT;
+    if (key < cnk) kb[key] = bv[j];
+  }
+  if (b == 0)
+    for (int e = threadIdx.x; e <= E; e += kPlanNT) offsets[e] = kbr[e];
+  if (w < cnw) group_count(wk, w, lane, cnk, cnb, ccnt);
+  __syncthreads();  // counts complete, kb and offsets written
+  group_prefix(cnw, cnk, ccnt, nullptr);
+  for (int e = threadIdx.x; e < E; e += kPlanNT) kbr[e] += base_r[(int64_t)e * nblk + b];
+  __syncthreads();
+  int dropped = 0;
+  // the routed grouping's keys: with the same wave split (nwr == cnw) each kept slot's expert replaces its
+  // capacity key in registers (-1 for a dropped slot); otherwise they are read back from the drop flags
+  const bool same_split = nwr == cnw;
+  if (w < cnw) {
+    if (same_split) {
+      group_rank_rekey(wk, w, lane, cnk, cnb, ccnt, [&](int64_t i, int key, int rank) {
+        const bool d = (int64_t)(kb[key] + rank) >= capacity;
+        drop[i] = d ? 1 : 0;
+        dropped += d ? 1 : 0;
+        return d ? -1 : key % E;
+      });
+    } else {
+      group_rank(wk, w, lane, cnk, cnb, ccnt,
+                 [&](int64_t i, int key, int rank) {
+                   const bool d = (int64_t)(kb[key] + rank) >= capacity;
+                   drop[i] = d ? 1 : 0;
+                   dropped += d ? 1 : 0;
+                 },
+                 [](int64_t) {});
+    }
+  }
+  const int t = block_sum(dropped, red);  // its barriers also make the block's drop flags visible to the block
+  if (threadIdx.x == 0 && t) atomicAdd(ndrop, t);
+  // the routed grouping of the kept slots
+  if (!same_split && w < nwr) load_keys(wk, beg, end, nwr, w, lane, pk, kRouted);
+  if (w < nwr) group_count(wk, w, lane, E, nbits, cnt);
+  __syncthreads();
+  group_prefix(nwr, E, cnt, nullptr);
+  __syncthreads();
+  if (w < nwr)
+    group_rank(wk, w, lane, E, nbits, cnt,
+               [&](int64_t i, int key, int rank) {
+                 const int row = kbr[key] + rank;  // < kbr[E] <= M (the guard only bounds the store)
+                 if (row < M) row_slot[row] = (int)i;
+                 slot_row[i] = row;
+               },
+               [&](int64_t i) { slot_row[i] = -1; });
+  const int kept_total = kbr[E];
+  for (int64_t r = kept_total + (int64_t)b * kPlanNT + threadIdx.x; r < M; r += (int64_t)nblk * kPlanNT)
+    row_slot[r] = -1;  // no row past the kept ones
+}
+
 __global__ void k_fill_i32(int* __restrict__ p, int n, int v) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
 }
@@ -954,7 +1142,7 @@ size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct PlanWs {
   int nblk_max, nkeys_max;
-  size_t off_counts, off_base, off_keytot, total;
+  size_t off_counts, off_base, off_keytot, off_base_r, total;
 };
 
 // Block tables of the multi-block path (plans the single-block planner does not take; those need none).
@@ -970,6 +1158,8 @@ PlanWs plan_ws(int64_t N, int64_t K, int64_t E) {
   off += al256((size_t)p.nblk_max * p.nkeys_max * 4);
   p.off_keytot = off;
   off += al256((size_t)(p.nkeys_max + 1) * 4);
+  p.off_base_r = off;  // the fused path's routed block bases [E][nblk]
+  off += al256((size_t)p.nblk_max * E * 4);
   p.total = off;
   return p;
 }
@@ -987,7 +1177,7 @@ int plan_allow_lds(Kern kernel, size_t bytes, std::atomic<size_t>& set_so_far) {
   }
   return 0;
 }
-std::atomic<size_t> g_lds_small{0}, g_lds_rank{0};
+std::atomic<size_t> g_lds_small{0}, g_lds_rank{0}, g_lds_rank2{0};
 
 // The grouping passes of the multi-block path.  `counted`: the counts table already holds this grouping's
 // block counts (written by the capacity rank pass before it).
@@ -1019,6 +1209,36 @@ struct Grouping {
     return check_launch("moe_plan grouping");
   }
 };
+
+// LDS of k_plan_rank2 (bytes).
+size_t plan_rank2_lds(int K, int E) {
+  const int cnk = K * E;
+  return (size_t)(plan_nwr(cnk) * cnk + cnk + plan_nwr(E) * E + E + 1 + kPlanNT + 16) * 4;
+}
+
+// Capacity drops with the routed layout in three launches (count, scan2, rank2) when the top-k and the rank
+// block's LDS allow it.
+bool plan_fused_ok(int64_t K, int64_t E) { return K <= kPlanMaxK && plan_rank2_lds((int)K, (int)E) <= 160 * 1024; }
+
+int plan_fused(hipStream_t s, const PlanKeys& pk, int64_t M, const PlanWs& p, char* ws, int64_t capacity,
+               uint8_t* drop, int* row_slot, int* slot_row, int* offsets, int* ndrop) {
+  const int K = pk.K, E = pk.E, nkeys = K * E;
+  const int nblk = (int)((M + kPlanIB - 1) / kPlanIB);
+  int* counts = reinterpret_cast<int*>(ws + p.off_counts);
+  int* base = reinterpret_cast<int*>(ws + p.off_base);
+  int* tot_r = reinterpret_cast<int*>(ws + p.off_keytot);
+  int* base_r = reinterpret_cast<int*>(ws + p.off_base_r);
+  MOE_LAUNCH("k_plan_count", k_plan_count, dim3(nblk), dim3(kPlanCountNT), (size_t)nkeys * 4, s, kCapacity, pk, M,
+             nkeys, nblk, counts, ndrop, 1);
+  MOE_LAUNCH("k_plan_scan2", k_plan_scan2, dim3((E + 3) / 4), dim3(256), 0, s, counts, nblk, K, E, capacity, base,
+             base_r, tot_r);
+  const size_t lds = plan_rank2_lds(K, E);
+  if (int rc = plan_allow_lds(k_plan_rank2, lds, g_lds_rank2)) return rc;
+  const PlanKeys pkr{pk.idx, drop, K, E};
+  MOE_LAUNCH("k_plan_rank2", k_plan_rank2, dim3(nblk), dim3(kPlanNT), lds, s, pkr, M, nblk, base, base_r, tot_r,
+             capacity, drop, row_slot, slot_row, offsets, ndrop);
+  return check_launch("moe_plan fused");
+}
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -1065,6 +1285,8 @@ int plan_run(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_t capaci
     return check_launch("moe_plan");
   }
   const PlanWs p = plan_ws(N, K, E);
+  if (drop && layout == 1 && plan_fused_ok(K, E))
+    return plan_fused(s, pk, M, p, ws, capacity, drop, row_slot, slot_row, offsets, ndrop);
   const Grouping g{s, pk, M, p, ws, drop, row_slot, slot_row, offsets, ndrop};
   if (drop) {
     // capacity drops; for the routed layout the same pass counts the kept slots per expert and block

@@ -47,6 +47,12 @@ CASES = [
     (16384, 1, 16, None, 1.0),  # the largest per-key plan
     (7, 2, 2, None, 0.0),
     (16385, 1, 8, None, 0.0),  # one slot more: the multi-block planner without drops
+    # capacity drops + routed layout beyond one block: count / scan2 / rank2
+    (70000, 8, 64, 0.5, 1.0),  # 274 planner blocks: scan2 carries its bases across block chunks of 256
+    (9000, 12, 32, 1.0, 2.0),  # K > 8: scan2 loads the keys of an expert in two rounds
+    (20000, 1, 128, 0.5, 3.0),  # K = 1, heavy drops, a ragged last block
+    (33000, 8, 128, 1.0, 3.0),  # C5-like keys (K*E = 1024), skewed
+    (5000, 8, 256, 1.0, 2.0),  # K*E = 2048: the capacity grouping on 8 waves, the routed one on 16
 ]
 
 
