@@ -636,10 +636,10 @@ __global__ __launch_bounds__(kPlanNT) void k_plan_rank(int mode, PlanKeys pk, in
 // Scan2: one wave per expert e.  For each block chunk of 256 blocks it loads the block counts of all K keys
 // (k, e) (eight keys per round of loads), writes the capacity bases base[key][b] (exclusive prefix over blocks,
 // carried across chunks in LDS), sums the kept slots per block over the K keys and writes their exclusive
-// prefix over blocks, base_r[e][b]; tot_r[e] = the expert's kept slots.
-__global__ __launch_bounds__(256) void k_plan_scan2(const int* __restrict__ counts, int nblk, int K, int E,
-                                                    int64_t capacity, int* __restrict__ base, int* __restrict__ base_r,
-                                                    int* __restrict__ tot_r) {
+// prefix over blocks, base_r[e][b]; tot_r[e] = the expert's kept slots.  base_r may be the counts table itself:
+// a lane writes base_r[e][b] only after it has loaded every count of expert e's keys in block b.
+__global__ __launch_bounds__(256) void k_plan_scan2(const int* counts, int nblk, int K, int E, int64_t capacity,
+                                                    int* __restrict__ base, int* base_r, int* __restrict__ tot_r) {
   __shared__ int s_run[4][kPlanMaxK];  // per wave: the running capacity base of each key (k, e)
   const int lane = threadIdx.x & 63, wq = threadIdx.x >> 6;
   const int e = blockIdx.x * 4 + wq;
@@ -1142,7 +1142,7 @@ size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct PlanWs {
   int nblk_max, nkeys_max;
-  size_t off_counts, off_base, off_keytot, off_base_r, total;
+  size_t off_counts, off_base, off_keytot, total;
 };
 
 // Block tables of the multi-block path (plans the single-block planner does not take; those need none).
@@ -1158,8 +1158,6 @@ PlanWs plan_ws(int64_t N, int64_t K, int64_t E) {
   off += al256((size_t)p.nblk_max * p.nkeys_max * 4);
   p.off_keytot = off;
   off += al256((size_t)(p.nkeys_max + 1) * 4);
-  p.off_base_r = off;  // the fused path's routed block bases [E][nblk]
-  off += al256((size_t)p.nblk_max * E * 4);
   p.total = off;
   return p;
 }
@@ -1227,7 +1225,9 @@ int plan_fused(hipStream_t s, const PlanKeys& pk, int64_t M, const PlanWs& p, ch
   int* counts = reinterpret_cast<int*>(ws + p.off_counts);
   int* base = reinterpret_cast<int*>(ws + p.off_base);
   int* tot_r = reinterpret_cast<int*>(ws + p.off_keytot);
-  int* base_r = reinterpret_cast<int*>(ws + p.off_base_r);
+  // the routed block bases [E][nblk] overwrite the block counts of the keys (0, e), which scan2's wave for
+  // expert e reads (and no other wave reads) before it writes them
+  int* base_r = counts;
   MOE_LAUNCH("k_plan_count", k_plan_count, dim3(nblk), dim3(kPlanCountNT), (size_t)nkeys * 4, s, kCapacity, pk, M,
              nkeys, nblk, counts, ndrop, 1);
   MOE_LAUNCH("k_plan_scan2", k_plan_scan2, dim3((E + 3) / 4), dim3(256), 0, s, counts, nblk, K, E, capacity, base,
