@@ -659,14 +659,19 @@ def add_mfma_ceiling(roof, extra, fp8):
     clock under that load), beside the published peak: ``roof["frac_of_ceiling"]`` is the kernel's share of it."""
     from moe_mi355 import _lib
 
+    peak = MFMA_FP8_PEAK_TFLOPS if fp8 else MFMA_BF16_PEAK_TFLOPS
     tf, mhz = _lib.prof_mfma_ceiling(100000, fp8=fp8)
+    tfr, mhzr = _lib.prof_mfma_ceiling(100000, fp8=fp8, random=True)
     roof["ceiling"] = round(tf, 1)
     roof["frac_of_ceiling"] = round(roof["achieved"] / tf, 4)
+    roof["ceiling_random_operands"] = round(tfr, 1)
+    roof["frac_of_ceiling_random_operands"] = round(roof["achieved"] / tfr, 4)
     extra["mfma_ceiling"] = {"instruction": "v_mfma_scale_f32_32x32x64_f8f6f4" if fp8 else "v_mfma_f32_32x32x16_bf16",
-                             "TFLOPs": round(tf, 1), "frac_of_peak": round(tf / (MFMA_FP8_PEAK_TFLOPS if fp8
-                                                                                   else MFMA_BF16_PEAK_TFLOPS), 4),
-                             "shader_MHz": round(mhz)}
-    log(f"[bench] MFMA ceiling ({'fp8' if fp8 else 'bf16'}): {tf:.0f} TFLOP/s at {mhz:.0f} MHz")
+                             "TFLOPs": round(tf, 1), "frac_of_peak": round(tf / peak, 4), "shader_MHz": round(mhz),
+                             "random_operands_TFLOPs": round(tfr, 1), "random_operands_frac_of_peak": round(tfr / peak, 4),
+                             "random_operands_shader_MHz": round(mhzr)}
+    log(f"[bench] MFMA ceiling ({'fp8' if fp8 else 'bf16'}): {tf:.0f} TFLOP/s at {mhz:.0f} MHz; random operands "
+        f"{tfr:.0f} TFLOP/s at {mhzr:.0f} MHz")
 
 
 _HBM_CEILING = {}

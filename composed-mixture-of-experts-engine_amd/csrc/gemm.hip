@@ -1033,33 +1033,64 @@ extern "C" int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, c
 // the dense MFMA rate the chip sustains and the shader clock it runs at under that load.
 // ---------------------------------------------------------------------------
 namespace moe {
-template <bool F8>
+// Bits of random-looking operand data (a 32-bit integer hash of the lane, fragment and element).
+__device__ __forceinline__ uint32_t ceil_hash(uint32_t v) {
+  v ^= v >> 16;
+  v *= 0x7feb352du;
+  v ^= v >> 15;
+  v *= 0x846ca68bu;
+  v ^= v >> 16;
+  return v;
+}
+
+// RAND: four independent A and four independent B fragments per lane, filled with hashed values (bf16: roughly
+// uniform in [-2, 2); e4m3: any finite byte), re-paired on every MFMA of a statically unrolled group of four
+// iterations, so consecutive MFMAs read different register data, as a data-carrying GEMM does; otherwise one A
+// and one B fragment of near-constant values.
+template <bool F8, bool RAND>
 __global__ __launch_bounds__(512) void k_mfma_ceiling(int iters, unsigned long long* __restrict__ stamps,
                                                       float* __restrict__ sink) {
   f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
-  i32x8 fa, fb;
-  bf16x8 ba, bb;
+  constexpr int NF = RAND ? 4 : 1;
+  i32x8 fa[NF], fb[NF];
+  bf16x8 ba[NF], bb[NF];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    fa[i] = 0x38383838 + (int)(threadIdx.x & 7);  // e4m3 bytes near 1.0
-    fb[i] = 0x30303030 + i;
-    ba[i] = (__bf16)(1e-3f * (float)(threadIdx.x + i));
-    bb[i] = (__bf16)(2e-3f * (float)i);
-  }
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (RAND) {
+        const uint32_t h = ceil_hash((threadIdx.x * 64u + (uint32_t)f * 8u + (uint32_t)i) * 2654435761u + blockIdx.x);
+        const uint32_t h2 = ceil_hash(h ^ 0x9e3779b9u);
+        fa[f][i] = (int)((h & 0x77777777u) | 0x08080808u);  // e4m3 bytes with exponent field < 15: finite
+        fb[f][i] = (int)((h2 & 0x77777777u) | 0x08080808u);
+        ba[f][i] = (__bf16)((float)(int)(h & 0xffffu) * (4.f / 65536.f) - 2.f);
+        bb[f][i] = (__bf16)((float)(int)(h2 & 0xffffu) * (4.f / 65536.f) - 2.f);
+      } else {
+        fa[f][i] = 0x38383838 + (int)(threadIdx.x & 7);  // e4m3 bytes near 1.0
+        fb[f][i] = 0x30303030 + i;
+        ba[f][i] = (__bf16)(1e-3f * (float)(threadIdx.x + i));
+        bb[f][i] = (__bf16)(2e-3f * (float)i);
+      }
+    }
+  auto step = [&](int p) __attribute__((always_inline)) {
+    // pairing p (0..NF-1): chain j multiplies A fragment (j + p) % NF by B fragment j
+    if constexpr (F8) {
+      c0 = mfma32x32x64_f8(fa[(0 + p) % NF], fb[0 % NF], c0);
+      c1 = mfma32x32x64_f8(fa[(1 + p) % NF], fb[1 % NF], c1);
+      c2 = mfma32x32x64_f8(fa[(2 + p) % NF], fb[2 % NF], c2);
+      c3 = mfma32x32x64_f8(fa[(3 + p) % NF], fb[3 % NF], c3);
+    } else {
+      c0 = mfma32x32x16(ba[(0 + p) % NF], bb[0 % NF], c0);
+      c1 = mfma32x32x16(ba[(1 + p) % NF], bb[1 % NF], c1);
+      c2 = mfma32x32x16(ba[(2 + p) % NF], bb[2 % NF], c2);
+      c3 = mfma32x32x16(ba[(3 + p) % NF], bb[3 % NF], c3);
+    }
+  };
   const unsigned long long t0 = __builtin_amdgcn_s_memtime();
   const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
-  for (int it = 0; it < iters; ++it) {
-    if constexpr (F8) {
-      c0 = mfma32x32x64_f8(fa, fb, c0);
-      c1 = mfma32x32x64_f8(fa, fb, c1);
-      c2 = mfma32x32x64_f8(fa, fb, c2);
-      c3 = mfma32x32x64_f8(fa, fb, c3);
-    } else {
-      c0 = mfma32x32x16(ba, bb, c0);
-      c1 = mfma32x32x16(ba, bb, c1);
-      c2 = mfma32x32x16(ba, bb, c2);
-      c3 = mfma32x32x16(ba, bb, c3);
-    }
+  for (int it = 0; it < iters; it += NF) {
+#pragma unroll
+    for (int p = 0; p < NF; ++p) step(p);
   }
   const unsigned long long t1 = __builtin_amdgcn_s_memtime();
   const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
@@ -1159,9 +1190,11 @@ extern "C" int moe_prof_hbm_ceiling(int64_t bytes, int mode, double* gbps) {
   return rc;
 }
 
-extern "C" int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, double* clock_mhz) {
-  if (iters < 1 || iters > (1 << 24) || !tflops || !clock_mhz)
-    return fail_arg("moe_prof_mfma_ceiling: bad arguments (1 <= iters <= 2^24, non-null outputs)");
+extern "C" int moe_prof_mfma_ceiling(int64_t iters, int mode, double* tflops, double* clock_mhz) {
+  if (iters < 1 || iters > (1 << 24) || mode < 0 || mode > 3 || !tflops || !clock_mhz)
+    return fail_arg("moe_prof_mfma_ceiling: bad arguments (1 <= iters <= 2^24, mode 0..3, non-null outputs)");
+  const bool fp8 = mode & 1, rnd = mode & 2;
+  iters = (iters + 3) / 4 * 4;  // the random-operand loop runs groups of four iterations
   int dev = 0;
   hipDeviceProp_t prop;
   if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
@@ -1178,10 +1211,14 @@ extern "C" int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, dou
     rc = check_launch("moe_prof_mfma_ceiling");
   } else {
     auto run = [&](int n) {
-      if (fp8)
-        hipLaunchKernelGGL(k_mfma_ceiling<true>, dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
+      if (fp8 && rnd)
+        hipLaunchKernelGGL((k_mfma_ceiling<true, true>), dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
+      else if (fp8)
+        hipLaunchKernelGGL((k_mfma_ceiling<true, false>), dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
+      else if (rnd)
+        hipLaunchKernelGGL((k_mfma_ceiling<false, true>), dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
       else
-        hipLaunchKernelGGL(k_mfma_ceiling<false>, dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
+        hipLaunchKernelGGL((k_mfma_ceiling<false, false>), dim3(blocks), dim3(512), 0, nullptr, n, d_st, d_sink);
     };
     run((int)std::min<int64_t>(iters, 2000));  // warm the clocks
     hipEventRecord(e0, nullptr);

@@ -148,10 +148,12 @@ def prof_summary() -> dict:
     return out
 
 
-def prof_mfma_ceiling(iters: int = 100000, fp8: bool = False) -> tuple:
-    """(TFLOP/s, shader MHz) of a memory-free MFMA loop on every CU of the current device."""
+def prof_mfma_ceiling(iters: int = 100000, fp8: bool = False, random: bool = False) -> tuple:
+    """(TFLOP/s, shader MHz) of a memory-free MFMA loop on every CU of the current device; ``random`` feeds
+    it changing, random-looking operands (as a data-carrying GEMM does) instead of near-constant ones."""
     tf, mhz = ctypes.c_double(0.0), ctypes.c_double(0.0)
-    check(load().moe_prof_mfma_ceiling(int(iters), 1 if fp8 else 0, ctypes.byref(tf), ctypes.byref(mhz)),
+    mode = (1 if fp8 else 0) | (2 if random else 0)
+    check(load().moe_prof_mfma_ceiling(int(iters), mode, ctypes.byref(tf), ctypes.byref(mhz)),
           "moe_prof_mfma_ceiling")
     return float(tf.value), float(mhz.value)
 

@@ -67,11 +67,15 @@ int moe_prof_kernel_name(int64_t i, char* buf, size_t len);
 
 /* MFMA ceiling of the current device (bench only; no counterpart in the
  * reference): one block of 8 waves per CU runs `iters` x 4 independent chains
- * of the grouped GEMM's MFMA (fp8 = 0: bf16 32x32x16; 1: e4m3 32x32x64) with no
- * memory traffic, timed with hipEvents on the null stream.  Returns the dense
- * rate in TFLOP/s and the shader clock under that load in MHz (s_memtime
- * ticks per 100 MHz s_memrealtime tick).  Allocates and synchronizes. */
-int moe_prof_mfma_ceiling(int64_t iters, int fp8, double* tflops, double* clock_mhz);
+ * of the grouped GEMM's MFMA with no memory traffic, timed with hipEvents on
+ * the null stream.  mode bit 0: the instruction (0: bf16 32x32x16; 1: e4m3
+ * 32x32x64); bit 1: the operands (0: one near-constant fragment pair; 1: four
+ * hashed fragment pairs re-paired on every MFMA, so the register data changes
+ * as in a data-carrying GEMM -- the part's power limit then sets a lower
+ * clock).  `iters` is rounded up to a multiple of 4.  Returns the dense rate
+ * in TFLOP/s and the shader clock under that load in MHz (s_memtime ticks per
+ * 100 MHz s_memrealtime tick).  Allocates and synchronizes. */
+int moe_prof_mfma_ceiling(int64_t iters, int mode, double* tflops, double* clock_mhz);
 
 /* HBM ceiling of the current device (bench only; no counterpart in the
  * reference): 10 timed grid-stride streams of 16-byte non-temporal accesses
