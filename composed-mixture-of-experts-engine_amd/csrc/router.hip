@@ -194,6 +194,147 @@ __device__ __forceinline__ void route_group(const f32x4 (&acc)[NT], int t0, int 
   }
 }
 
+// Routing of one 16-token group with four lanes per token (the wide forward, NT = 4 or 8 tiles of 16 experts).
+// acc[nt][i] = logits[t0 + 4g + i][nt*16 + n] (16x16 MFMA layout, lane = 16g + n).  The bias, the logits / nf
+// outputs and the NaN mapping happen in that layout (64-byte row segments); the cleaned logits then go through
+// `tile` (the wave's own LDS, 16 rows of NT*16 + 4 floats: the padding puts the 16 rows of one column group in
+// different bank groups) so that lane 4r + s holds the 4*NT logits of token t0 + r at experts 4j + s.  Softmax,
+// top-k (K rounds of a strict arg-max over order-preserving keys: within a lane the lowest j wins a tie, across
+// the quad the lowest expert id) and renormalisation run on those with 2-step quad reductions (DPP), where the
+// 16-lane form needs 4 steps per round and handles 4 tokens per lane in turn.  Round r's pick is kept by lane
+// s = r % 4 in slot r / 4.  The probabilities go back through the tile to be summed per expert over the group
+// in the MFMA layout.  Outputs and statistics (s_cnt, s_p, s_z, s_nf) as route_group's.
+template <int NT>
+__device__ __forceinline__ void route_quad(const f32x4 (&acc)[NT], float* tile, int t0, int lane,
+                                           const float* __restrict__ bias, int N, int E, int K,
+                                           int64_t* __restrict__ idx_out, void* __restrict__ w_out, int w_dt,
+                                           float* __restrict__ logits_out, float* __restrict__ lse_out, int* s_cnt,
+                                           float* s_p, float* s_z, int* s_nf) {
+  constexpr int L = 4 * NT;       // logits per lane
+  constexpr int P = NT * 16 + 4;  // tile row pitch (floats)
+  constexpr int KS = kMaxK / 4;   // pick slots per lane
+  const int g = lane >> 4, n = lane & 15;
+  int nf = 0;
+  {
+    float bv[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) bv[nt] = (bias != nullptr) ? bias[min(nt * 16 + n, E - 1)] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tt = t0 + g * 4 + i;
+      const bool valid = tt < N;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int e = nt * 16 + n;
+        float v = acc[nt][i] + bv[nt];
+        if (valid && e < E) {
+          logits_out[(int64_t)tt * E + e] = v;
+          if (!isfinite(v)) ++nf;
+        }
+        if (v != v || e >= E) v = -INFINITY;  // NaN (and experts past E) never win a top-k slot
+        tile[(4 * g + i) * P + nt * 16 + n] = v;
+      }
+    }
+  }
+  __asm__ volatile("" ::: "memory");  // the wave's LDS accesses complete in order: the tile is written
+  const int r = lane >> 2, s = lane & 3;
+  const int tt = t0 + r;
+  const bool valid = tt < N;
+  float lg[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) lg[j] = tile[r * P + 4 * j + s];
+  float m = lg[0];
+#pragma unroll
+  for (int j = 1; j < L; ++j) m = fmaxf(m, lg[j]);
+  m = fmaxf(m, row16_partner<0>(m));
+  m = fmaxf(m, row16_partner<1>(m));
+  float ex[L], sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    ex[j] = expf(lg[j] - m);
+    sum += ex[j];
+  }
+  sum += row16_partner<0>(sum);
+  sum += row16_partner<1>(sum);
+  const float inv = 1.f / sum;
+  const float lse = m + logf(sum);
+  if (valid && s == 0) lse_out[tt] = lse;
+  uint32_t kh[L];
+#pragma unroll
+  for (int j = 0; j < L; ++j) kh[j] = (4 * j + s < E) ? order_key(lg[j]) : 0u;
+  int e_slot[KS];
+  float p_slot[KS];
+#pragma unroll
+  for (int q = 0; q < KS; ++q) {
+    e_slot[q] = 0;
+    p_slot[q] = 0.f;
+  }
+  float psum = 0.f;
+  for (int rr = 0; rr < K; ++rr) {
+    uint32_t bh = kh[0];
+    int bj = 0;
+#pragma unroll
+    for (int j = 1; j < L; ++j) {  // strict '>' keeps the lower j (lower expert) on a tie
+      const bool t = kh[j] > bh;
+      bh = t ? kh[j] : bh;
+      bj = t ? j : bj;
+    }
+    int be = bh ? 4 * bj + s : 0x7fffffff;
+    const uint32_t w1 = max(bh, (uint32_t)row16_partner<0>((int)bh));
+    const uint32_t wmax = max(w1, (uint32_t)row16_partner<1>((int)w1));
+    be = bh == wmax ? be : 0x7fffffff;
+    be = min(be, row16_partner<0>(be));
+    be = min(be, row16_partner<1>(be));
+#pragma unroll
+    for (int j = 0; j < L; ++j) kh[j] = (4 * j + s == be) ? 0u : kh[j];  // the winner's lane
+    const float pv = expf(order_val(wmax) - m) * inv;
+    psum += pv;
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      e_slot[q] = rr == 4 * q + s ? be : e_slot[q];
+      p_slot[q] = rr == 4 * q + s ? pv : p_slot[q];
+    }
+  }
+  const float rden = 1.f / fmaxf(psum, 1e-30f);
+  if (valid) {
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      const int rr = 4 * q + s;
+      if (rr < K) {
+        idx_out[(int64_t)tt * K + rr] = e_slot[q];
+        store_f(w_out, w_dt, (int64_t)tt * K + rr, p_slot[q] * rden);
+        atomicAdd(&s_cnt[e_slot[q]], 1);
+      }
+    }
+  }
+  // the token's probabilities back through the tile, summed per expert over the group's 16 tokens
+  __asm__ volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < L; ++j) tile[r * P + 4 * j + s] = valid ? ex[j] * inv : 0.f;
+  __asm__ volatile("" ::: "memory");
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v += tile[(4 * g + i) * P + nt * 16 + n];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (g == 0) s_p[nt * 16 + n] = v;
+  }
+  float zacc = (valid && s == 0) ? lse * lse : 0.f;
+  zacc += __shfl_xor(zacc, 1);
+  zacc += __shfl_xor(zacc, 2);
+  zacc += __shfl_xor(zacc, 4);
+  zacc += __shfl_xor(zacc, 8);
+  zacc += __shfl_xor(zacc, 16);
+  zacc += __shfl_xor(zacc, 32);
+  nf = wave_sum(nf);
+  if (lane == 0) {
+    *s_z = zacc;
+    *s_nf = nf;
+  }
+}
+
 // Routing of a block's 16*TG tokens with one lane per token (E <= EP, EP = 8 or 16), called by every thread of
 // the 512-thread block.  The 8 waves' partial logit tiles (s_accf: wave w's TG 16x16 tiles in MFMA layout,
 // TG*256 floats) are summed in wave order into s_lg [16*TG][17] (rows padded: the per-token reads below hit
@@ -744,7 +885,9 @@ __global__ __launch_bounds__(512) void k_router_fwd_wide(
   constexpr int O_CNT = 0, O_P = O_CNT + NT * 16 * 4, O_Z = O_P + TG * NT * 16 * 4, O_NF = O_Z + TG * 4;
   constexpr int O_LAST = O_NF + TG * 4, O_FIN = O_LAST + 16;
   constexpr int EPI = O_FIN + finalize_scratch_floats<512>() * 4;
-  static_assert(RING >= EPI, "ring too small for the epilogue arrays");
+  // NT <= 8: each wave's routing tile (16 rows of NT*16 + 4 floats) after the epilogue arrays
+  constexpr int O_TR = (EPI + 15) & ~15, TRB = 16 * (NT * 16 + 4) * 4;
+  static_assert(RING >= (NT <= 8 ? O_TR + TG * TRB : EPI), "ring too small for the epilogue arrays");
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING];
   int* s_cnt = reinterpret_cast<int*>(ring + O_CNT);
   float(*s_p)[NT * 16] = reinterpret_cast<float(*)[NT * 16]>(ring + O_P);
@@ -808,8 +951,14 @@ __global__ __launch_bounds__(512) void k_router_fwd_wide(
 
   for (int i = threadIdx.x; i < NT * 16; i += 512) s_cnt[i] = 0;
   __syncthreads();
-  route_group<NT>(acc, t0 + 16 * wv, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt, s_p[wv],
-                  &s_z[wv], &s_nf[wv]);
+  if constexpr (NT <= 8) {
+    float* tile = reinterpret_cast<float*>(ring + O_TR + wv * TRB);
+    route_quad<NT>(acc, tile, t0 + 16 * wv, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt,
+                   s_p[wv], &s_z[wv], &s_nf[wv]);
+  } else {
+    route_group<NT>(acc, t0 + 16 * wv, lane, bias, N, E, K, idx_out, w_out, w_dt, logits_out, lse_out, s_cnt,
+                    s_p[wv], &s_z[wv], &s_nf[wv]);
+  }
   __syncthreads();
   fwd_block_tail<TG, NT>(s_cnt, s_p, s_z, s_nf, s_last, s_fin, N, E, K, part_cnt, part_p, part_z, ticket, aux_coef,
                          z_coef, cnt_out, stats, aux_out, z_out);

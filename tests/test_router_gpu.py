@@ -45,6 +45,8 @@ SHAPES = [
     (96, 96, 64, 4, torch.bfloat16, torch.bfloat16),      # H % 64 != 0 -> packed-gate kernel
     (100, 96, 10, 3, torch.bfloat16, torch.bfloat16),     # E not a multiple of 16
     (128, 256, 40, 18, torch.bfloat16, torch.bfloat16),   # K > 16 on the MFMA path
+    (300, 256, 64, 32, torch.bfloat16, torch.bfloat16),   # K = 32 (the largest) on the wide kernel, E = 64
+    (170, 256, 128, 12, torch.bfloat16, torch.bfloat16),  # K = 12 on the wide kernel, E = 128 (K = 32 there: the ties test)
     (50, 72, 8, 2, torch.bfloat16, torch.bfloat16),       # H % 32 != 0 -> generic path
     (333, 256, 24, 20, torch.float32, torch.float32),     # K > 16; fp32 forward, generic backward (E > 16)
     (200, 64, 8, 2, torch.bfloat16, torch.float32),       # mixed dtypes -> generic path
@@ -171,15 +173,32 @@ def test_router_deterministic():
         assert torch.equal(a, b)
 
 
-def test_router_exact_ties_take_lowest_index():
-    say("[router ties]")
+@pytest.mark.parametrize("N,H,E,K", [(100, 64, 8, 3), (300, 256, 64, 6), (200, 512, 128, 8), (150, 256, 64, 32),
+                                     (120, 256, 128, 32)])
+def test_router_exact_ties_take_lowest_index(N, H, E, K):
+    """All logits equal: the first K experts in order.  Gate columns equal in pairs (2j, 2j + 1): the device
+    logits of a pair are bit-identical, so the picks come in pairs, the lower id first.  E > 32 runs the wide
+    streaming forward."""
+    say(f"[router ties] N={N} H={H} E={E} K={K}")
     d = dev()
-    N, H, E, K = 100, 64, 8, 3
     x = torch.randn(N, H).to(torch.bfloat16).to(d)
     w = torch.zeros(H, E, dtype=torch.bfloat16, device=d)
     idx, wt, *_ = ops.router_forward(x, w, K)
     assert torch.equal(idx.cpu(), torch.arange(K).expand(N, K))
     assert torch.allclose(wt.float().cpu(), torch.full((N, K), 1.0 / K), atol=1e-3)
+    if K % 2:
+        return
+    g = torch.Generator().manual_seed(E + K)
+    w = (torch.randn(H, E // 2, generator=g) * 0.05).to(torch.bfloat16).repeat_interleave(2, dim=1).to(d)
+    idx, wt, logits, *_ = ops.router_forward(x, w, K)
+    idx, wt, logits = idx.cpu(), wt.float().cpu(), logits.float().cpu()
+    assert torch.equal(logits[:, 0::2], logits[:, 1::2])
+    assert torch.equal(idx[:, 0::2] % 2, torch.zeros(N, K // 2, dtype=idx.dtype))
+    assert torch.equal(idx[:, 1::2], idx[:, 0::2] + 1)
+    assert torch.equal(wt[:, 0::2], wt[:, 1::2])
+    # the picked pairs are the K / 2 largest pair logits, in descending order
+    top = logits[:, 0::2].topk(K // 2, dim=-1).values
+    assert torch.equal(logits.gather(1, idx[:, 0::2]), top)
 
 
 def test_router_with_bias_matches_oracle():
