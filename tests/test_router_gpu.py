@@ -266,3 +266,40 @@ def test_router_fp32_unaligned_x_takes_the_generic_kernels(losses):
     ref = OR.router_full(x, w, K, grad_w=gw, alpha=alpha, beta=beta, idx_override=idx.cpu())
     assert_rel(xv.grad, ref["dX"], 1e-5, "dX", floor=1e-4)
     assert_rel(wd_.grad, ref["dW"], 1e-5, "dW", floor=1e-4)
+
+
+@pytest.mark.parametrize("N,H,E,K,dt", [
+    (300, 256, 8, 2, torch.bfloat16),     # E <= 16 streaming forward (one lane per token)
+    (300, 256, 64, 6, torch.bfloat16),    # wide forward, four lanes per token
+    (260, 512, 128, 8, torch.bfloat16),   # wide forward, four lanes per token, 8 expert tiles
+    (200, 128, 256, 8, torch.bfloat16),   # wide forward, 16 lanes per token
+    (300, 256, 16, 4, torch.float32),     # fp32 MFMA forward
+], ids=lambda v: str(v)[6:] if isinstance(v, torch.dtype) else str(v))
+def test_router_nan_gate_column_is_never_picked(N, H, E, K, dt):
+    """A NaN in one gate column makes that expert's logit NaN for every token.  Every forward path maps it to
+    -inf for the softmax and the top-k: the expert is never picked and gets probability 0, the weights stay
+    finite, the stored logits keep the NaN and the non-finite count is N.  The indices and weights are those
+    of the float64 oracle with that expert's logit at -inf (a -inf bias)."""
+    from moe_mi355.router import STAT_NONFINITE
+    say(f"[router nan column] N={N} H={H} E={E} K={K} {dt}")
+    d = dev()
+    x, w, _ = _inputs(N, H, E, K, dt, dt, seed=E + 1)
+    e0 = E // 2 + 1
+    w_nan = w.clone()
+    w_nan[5, e0] = float("nan")
+    idx, wt, logits, lse, cnt, stats = ops.router_forward(x.to(d), w_nan.to(d), K)
+    torch.cuda.synchronize()
+    idx, wt, logits, stats = idx.cpu(), wt.float().cpu(), logits.cpu(), stats.float().cpu()
+    others = [e for e in range(E) if e != e0]
+    assert torch.isnan(logits[:, e0]).all()
+    assert torch.isfinite(logits[:, others]).all()
+    assert not bool((idx == e0).any())
+    assert torch.isfinite(wt).all()
+    assert float(stats[STAT_NONFINITE]) == N
+    bias = torch.zeros(E, dtype=torch.float64)
+    bias[e0] = float("-inf")
+    ref = OR.route_fwd(x, w, K, bias=bias)
+    ok = ref["margin"] > MARGIN
+    assert ok.float().mean() > 0.9
+    assert torch.equal(idx[ok], ref["idx"][ok])
+    assert_rel(wt[ok], ref["w"][ok], TOL[dt], "weights")
