@@ -65,12 +65,28 @@ def log(*a):
 
 
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_counters.md")
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
+
+
+def kernel_src_digest():
+    """sha256 over the GPU kernel sources (csrc/*.hip and csrc/*.h, sorted by name): the identity of the
+    kernels a counter summary was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC_DIR)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(CSRC_DIR, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()
 
 
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of ``kernel`` on ``workload`` from the committed counter summary
     (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain
-    copy of known size), or None when the summary has no entry for it."""
+    copy of known size), or None when the summary has no entry for it or was measured on other
+    kernel sources than the ones built here (its ``kernel_src_sha256`` differs)."""
     try:
         with open(TRAFFIC_FILE) as f:
             text = f.read()
@@ -84,10 +100,32 @@ def measured_traffic(kernel, workload):
         data = json.loads(text[start + 7:end])
     except ValueError:
         return None
+    if data.get("kernel_src_sha256") != kernel_src_digest():
+        log(f"[bench] {os.path.relpath(TRAFFIC_FILE, REPO)} was measured on other kernel sources: "
+            "roofline.traffic left null")
+        return None
     ent = data.get("workloads", {}).get(workload, {}).get(kernel)
     if ent is None:
         return None
     return int(ent["fetch_bytes"] + ent["write_bytes"])
+
+
+def cpu_thread_count():
+    """Threads for the CPU baselines: every core this process may run on (its affinity set), or fewer when
+    the host sets OMP_NUM_THREADS (the GPU box grants each GPU a share of its cores and sets it to that)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(n, 1)
+
+
+def cpu_cores(torch):
+    """The core-count fields of a cpu_baseline record: the threads the baseline ran with, and the host's
+    os.cpu_count() and affinity set beside it."""
+    return {"cores": torch.get_num_threads(), "host_cpu_count": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
 def copy_probe(torch):
@@ -233,26 +271,21 @@ def run_router(args, torch):
     }
 
 
-def cpu_baseline_router(torch, budget_s=12.0):
+def cpu_baseline_router(torch):
+    """The float64 oracle of the whole C2 router step (forward + backward, same seed) on the host's cores, timed
+    the reference's way: 3 warmup + 20 timed calls, mean +- std (run_benchmark.py L:63-79)."""
     from oracle import router as OR
 
     from moe_mi355 import configs
 
     cfg = configs.C2
-    sample_T = 4096
-    inp = configs.router_inputs(cfg.scaled(sample_T))
+    inp = configs.router_inputs(cfg)
     x, w, gw = inp["x"], inp["gate_w"], inp["grad_w"]
-    OR.router_full(x, w, cfg.K, grad_w=gw)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        OR.router_full(x, w, cfg.K, grad_w=gw)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
-            break
-    return {"value": n * sample_T / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"float64 oracle router fwd+bwd (oracle/router.py router_full) on {sample_T} tokens of C2 "
-                      f"(same seed), {n} reps in {el:.1f} s"}
+    mean, std = mean_std_ms(lambda: OR.router_full(x, w, cfg.K, grad_w=gw))
+    return {"value": cfg.T / (mean * 1e-3), "unit": "tokens/s", **cpu_cores(torch), "kind": "port",
+            "ms_mean": round(mean, 2), "ms_std": round(std, 2),
+            "sample": f"the whole C2 config: float64 oracle router fwd+bwd (oracle/router.py router_full), "
+                      f"T={cfg.T} d={cfg.H} E={cfg.E} K={cfg.K}, seed {cfg.seed}, 3 warmup + 20 timed calls"}
 
 
 # ---------------------------------------------------------------------------
@@ -291,7 +324,7 @@ def run_c1(args, torch, with_cpu=True):
         xc, wc, gc = inp["x"], inp["gate_w"], inp["grad_w"]
         cm, cs = mean_std_ms(lambda: OR.router_full(xc, wc, K, grad_w=gc, alpha=cfg.aux_coef, beta=cfg.z_coef))
         res["cpu_baseline"] = {
-            "value": N / (cm * 1e-3), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "value": N / (cm * 1e-3), "unit": "tokens/s", **cpu_cores(torch), "kind": "port",
             "ms_mean": round(cm, 3), "ms_std": round(cs, 3),
             "sample": "the whole C1 config: float64 oracle router fwd+bwd with aux and z losses (oracle/router.py "
                       "router_full), T=4096 d=512 E=8 K=2, seed 0, 3 warmup + 20 timed calls"}
@@ -485,7 +518,7 @@ def cpu_baseline_layer(torch, cfg, layout, inp, sample_T=32, budget_s=12.0, min_
     mean = sum(times) / len(times)
     std = (sum((t - mean) ** 2 for t in times) / len(times)) ** 0.5
     del f64
-    return {"value": sample_T / mean, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": sample_T / mean, "unit": "tokens/s", **cpu_cores(torch), "kind": "port",
             "ms_mean": round(mean * 1e3, 1), "ms_std": round(std * 1e3, 1),
             "sample": f"float64 oracle layer fwd+bwd (oracle/layer.py layer_fwd_bwd) on the first {sample_T} "
                       f"tokens of {cfg.name} with the full-size expert weights (converted to float64 before "
@@ -648,7 +681,7 @@ def cpu_baseline_dispatch(torch, cfg, inp, sample_T=8192, budget_s=6.0):
         times.append(time.perf_counter() - a)
     mean = sum(times) / len(times)
     std = (sum((t - mean) ** 2 for t in times) / len(times)) ** 0.5
-    return {"value": sample_T / mean, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": sample_T / mean, "unit": "tokens/s", **cpu_cores(torch), "kind": "port",
             "ms_mean": round(mean * 1e3, 1), "ms_std": round(std * 1e3, 1),
             "sample": f"first {sample_T} tokens of C3: float64 oracle routing + oracle drop mask and routed plan "
                       f"+ float32 torch permute and combine, {len(times)} reps after 1 warmup"}
@@ -731,7 +764,7 @@ def main():
         sys.exit(2)
     import torch
 
-    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cpu_thread_count())
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)

@@ -714,9 +714,11 @@ __global__ __launch_bounds__(256) void k_plan_scan2(const int* counts, int nblk,
 // LDS: ccnt [cnw * K*E] + kb [K*E] + cnt [nwr * E] + kbr [E + 1] + part [1024] + red [16] ints.
 __global__ __launch_bounds__(kPlanNT) void k_plan_rank2(PlanKeys pk, int64_t M, int nblk, const int* __restrict__ base,
                                                         const int* __restrict__ base_r, const int* __restrict__ tot_r,
-                                                        int64_t capacity, uint8_t* __restrict__ drop,
+                                                        int64_t capacity, uint8_t* drop,
                                                         int* __restrict__ row_slot, int* __restrict__ slot_row,
                                                         int* __restrict__ offsets, int* __restrict__ ndrop) {
+  // `drop` is not restrict-qualified: when the two groupings split the block differently the routed pass reads
+  // the flags written here back through pk.drop, the same bytes
   extern __shared__ int lds[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int K = pk.K, E = pk.E;

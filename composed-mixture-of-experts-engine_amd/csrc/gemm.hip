@@ -446,9 +446,10 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     // kt is computed, each wave writes its share of slice kt+1 (loaded during slice kt-1) into the free LDS
     // slot and loads its share of slice kt+2 into the same registers, one piece (16 bytes a lane) at a time
     // between the MFMAs, so global loads, LDS writes and fragment reads are spread over the slice.  The loads
-    // are issued from asm, so the compiler does not drain them before the first LDS write: piece p of slice
-    // kt+1 was loaded NP loads before piece p of slice kt+2, and loads complete in order, so vmcnt(NP-1)
-    // before its write suffices (vmcnt(NP-1-p) once no new load follows).
+    // are ordinary global loads through an address_space(1) pointer: the compiler sees each load's destination
+    // st[p] and places the vmcnt wait before the LDS write that reads it (piece p of slice kt+1 was loaded NP
+    // loads before piece p of slice kt+2, so that wait is vmcnt(NP-1) and leaves the newer loads in flight).
+    // The loop has no explicit vmcnt wait of its own; a load issued from asm here would need one.
     constexpr int NP = 2 * QPW;  // pieces per wave per slice: A pieces 0..QPW-1, then B
     u32x4 st[NP];
     // source of piece p of slice kt; `full`: the slice lies inside the reduction range and on one side of

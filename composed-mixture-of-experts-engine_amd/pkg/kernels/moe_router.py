@@ -312,7 +312,12 @@ class MoERouter(torch.nn.Module):
             # recomputed under no_grad, so no gradient flows through w; _last_logits
             # and the reported z statistic are computed without the bias (L:727-733).
             w = w.detach()
-            logits = logits - self.bias.detach().float()
+            # the bias-free logits as the reference forms them (x and gate in fp32, one product), not the
+            # kernel's biased logits minus the bias, which would carry ~ulp(|bias|) of cancellation error
+            with torch.no_grad():
+                logits = flat.detach().float() @ self.gate_w.detach().float()
+                if self.logit_bias is not None:
+                    logits = logits + self.logit_bias.float()
             z_plain = torch.logsumexp(logits, dim=-1).square().mean().reshape(1) if N else logits.new_zeros(1)
         self._last_logits = logits
         self.last_aux_loss = aux
