@@ -49,6 +49,17 @@ __device__ __forceinline__ uint32_t pack2bf(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
 }
 
+// Sum of two rows of 8 bf16 (one 16-byte word each) in fp32, rounded to bf16: the result of adding the two
+// bf16 tensors (each pair is widened exactly, summed in fp32 and rounded to nearest even once).
+__device__ __forceinline__ u32x4 add_bf16x8(const u32x4& v, const u32x4& a) {
+  u32x4 r;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    r[d] = pack2bf(__uint_as_float(v[d] << 16) + __uint_as_float(a[d] << 16),
+                   __uint_as_float(v[d] & 0xffff0000u) + __uint_as_float(a[d] & 0xffff0000u));
+  return r;
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

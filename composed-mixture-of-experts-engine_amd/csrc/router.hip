@@ -1612,6 +1612,7 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NTE ==
                                                             const float* __restrict__ grad_z, float aux_coef,
                                                             float z_coef, int N, int H, int E, int K, int tc_len,
                                                             int nht, uint16_t* __restrict__ dx,
+                                                            const uint16_t* __restrict__ dx_add,
                                                             float* __restrict__ ws_dw, uint16_t* __restrict__ g_out,
                                                             int g_pitch) {
   constexpr int GS = NTE * 16;       // expert slots of a token-major G row
@@ -1642,6 +1643,15 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NTE ==
     for (int j = 0; j < 4; ++j) {
       const int t = ts0 + (lane >> 3) + 8 * j;
       r[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xw + (int64_t)min(t, tend - 1) * H));
+    }
+  };
+  // the same rows of an [N, H] bf16 tensor (the dx addend), same clamping
+  auto load_rows = [&](const uint16_t* src, u32x4(&r)[4], int ts0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = ts0 + (lane >> 3) + 8 * j;
+      r[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(src + col0 + (lane & 7) * 8 + (int64_t)min(t, tend - 1) * H));
     }
   };
   // ---- G = dL/dlogits of the chunk, one token per thread, rounded to bf16 as the reference does
@@ -1768,6 +1778,10 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NTE ==
       *reinterpret_cast<u32x4*>(&xsw[((lane >> 3) + 8 * j) * kSXP + (lane & 7) * 8]) =
           u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
     }
+    // the addend rows of this step's dx, requested before the x refill so that waiting for them at the
+    // stores leaves the refill in flight (loads complete in order)
+    u32x4 ad[4];
+    if (dx_add != nullptr) load_rows(dx_add, ad, tbeg + lr0);
     load_x(r, tbeg + lr0 + 64);
     // dwg: D[m = h][n = e] += sum_t x[t][h] G[t][e]; A from two transposing reads: x[8g .. 8g+7][mt*16 + n]
 #pragma unroll
@@ -1801,7 +1815,8 @@ __global__ __launch_bounds__(64 * WPB) __attribute__((amdgpu_waves_per_eu(NTE ==
     for (int j = 0; j < 4; ++j) {
       const int lr = (lane >> 3) + 8 * j;
       const int t = tbeg + lr0 + lr;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&xsw[lr * kSXP + (lane & 7) * 8]);
+      u32x4 v = *reinterpret_cast<const u32x4*>(&xsw[lr * kSXP + (lane & 7) * 8]);
+      if (dx_add != nullptr) v = add_bf16x8(v, ad[j]);
       if (t < tend) *reinterpret_cast<u32x4*>(dx + (int64_t)t * H + col0 + (lane & 7) * 8) = v;
     }
   };
@@ -1845,6 +1860,7 @@ __global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __rest
                                                           const uint16_t* __restrict__ wg,
                                                           const uint16_t* __restrict__ gb, int N, int H, int E,
                                                           int tc_len, int nht, uint16_t* __restrict__ dx,
+                                                          const uint16_t* __restrict__ dx_add,
                                                           float* __restrict__ ws_dw) {
   constexpr int EKP = EK * 32;
   constexpr int GP = wide_gpitch<EK>();  // G tile pitch (bf16): 16-byte rows, conflict-free reads below
@@ -1874,6 +1890,15 @@ __global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __rest
     for (int j = 0; j < 4; ++j) {
       const int t = ts0 + (lane >> 3) + 8 * j;
       r[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xw + (int64_t)min(t, tend - 1) * H));
+    }
+  };
+  // the same rows of an [N, H] bf16 tensor (the dx addend), same clamping
+  auto load_rows = [&](const uint16_t* src, u32x4(&r)[4], int ts0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = ts0 + (lane >> 3) + 8 * j;
+      r[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(src + col0 + (lane & 7) * 8 + (int64_t)min(t, tend - 1) * H));
     }
   };
   // G stream: unit q = tid + 256 j of the step is row q / GU, 16-byte unit q % GU
@@ -1936,6 +1961,8 @@ __global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __rest
       *reinterpret_cast<u32x4*>(&xsw[((lane >> 3) + 8 * j) * kSXP + (lane & 7) * 8]) =
           u32x4{ok ? v[0] : 0u, ok ? v[1] : 0u, ok ? v[2] : 0u, ok ? v[3] : 0u};
     }
+    u32x4 ad[4];  // this step's dx addend rows, requested before the x refill (see the streaming form)
+    if (dx_add != nullptr) load_rows(dx_add, ad, tbeg + lr0);
     load_x(r, tbeg + lr0 + 64);
     lds_sync();  // the step's G tile is visible to every wave (and every wave is done with step s-1)
     // dwg: D[m = h][n = e] += sum_t x[t][h] G[t][e]; A = x^T and B = G^T from transposing reads
@@ -1978,7 +2005,8 @@ __global__ __launch_bounds__(256) void k_router_dxdw_wide(const uint16_t* __rest
     for (int j = 0; j < 4; ++j) {
       const int lr = (lane >> 3) + 8 * j;
       const int t = tbeg + lr0 + lr;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&xsw[lr * kSXP + (lane & 7) * 8]);
+      u32x4 v = *reinterpret_cast<const u32x4*>(&xsw[lr * kSXP + (lane & 7) * 8]);
+      if (dx_add != nullptr) v = add_bf16x8(v, ad[j]);
       if (t < tend)
         __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dx + (int64_t)t * H + col0 + (lane & 7) * 8));
     }
@@ -2294,6 +2322,20 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t E, int x_dt, int w_dt) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// dx += dx_add element-wise (same dtype; a bf16 sum is formed in fp32 and rounded once, as a tensor addition
+// is), for the backward forms that do not fold the addend into their dx stores.
+__global__ __launch_bounds__(256) void k_add_rows(void* __restrict__ dx, const void* __restrict__ add, int64_t n,
+                                                  int dt) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+    store_f(dx, dt, i, load_f(dx, dt, i) + load_f(add, dt, i));
+}
+
+void launch_add_rows(hipStream_t s, void* dx, const void* add, int64_t n, int dt) {
+  MOE_LAUNCH("k_add_rows", k_add_rows, dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(16384, (n + 255) / 256))),
+             dim3(256), 0, s, dx, add, n, dt);
+}
+
 void launch_reduce(hipStream_t s, const float* ws, int nchunk, int64_t len, void* out, int out_dt) {
   if (len % 4 == 0) {
     const unsigned nb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (len / 4 + 63) / 64));
@@ -2327,12 +2369,12 @@ template <int NTE>
 void launch_dxdw_stream(hipStream_t s, const uint16_t* x, const uint16_t* wg, const float* logits, const int64_t* idx,
                         const void* gw, int gw_dt, const int64_t* cnt, const float* grad_aux, const float* grad_z,
                         float aux_coef, float z_coef, int N, int H, int E, int K, int tc_len, int nchunk, uint16_t* dx,
-                        float* ws, uint16_t* g_out = nullptr, int g_pitch = 0) {
+                        float* ws, uint16_t* g_out = nullptr, int g_pitch = 0, const uint16_t* dx_add = nullptr) {
   const char* name = dx ? "k_router_dxdw_bf16" : "k_router_dw_bf16";
 #define MOE_DXDW_STREAM(EL_, KR_, WPB_)                                                                               \
   MOE_LAUNCH(name, (k_router_dxdw_stream<NTE, EL_, KR_, WPB_>), dim3((unsigned)(nchunk * (H / (64 * WPB_)))),          \
              dim3(64 * WPB_), 0, s, x, wg, logits, idx, gw, gw_dt, cnt, grad_aux, grad_z, aux_coef, z_coef, N, H, E, K,  \
-             tc_len, H / (64 * WPB_), dx, ws, g_out, g_pitch)
+             tc_len, H / (64 * WPB_), dx, dx_add, ws, g_out, g_pitch)
   // G over 8 expert slots when E <= 8 (fewer registers while the first x tiles are in flight); the top-k
   // slots preloaded: 2 when K <= 2 (shorter code: the prologue runs on a cold instruction cache), else 4;
   // 16-wave blocks (1024 columns) when H allows
@@ -2557,11 +2599,11 @@ extern "C" size_t moe_router_bwd_workspace(int64_t N, int64_t H, int64_t E, int6
   return plan_bwd(N, H, E, x_dtype, wg_dtype).total;
 }
 
-extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* logits,
-                              const int64_t* idx, const void* grad_w, int gw_dtype, const int64_t* cnt,
-                              const float* grad_aux, const float* grad_z, float aux_coef, float z_coef, int64_t N,
-                              int64_t H, int64_t E, int64_t K, void* dx_out, void* dwg_out, void* workspace,
-                              size_t ws_bytes, void* stream) {
+extern "C" int moe_router_bwd_acc(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* logits,
+                                  const int64_t* idx, const void* grad_w, int gw_dtype, const int64_t* cnt,
+                                  const float* grad_aux, const float* grad_z, float aux_coef, float z_coef, int64_t N,
+                                  int64_t H, int64_t E, int64_t K, const void* dx_add, void* dx_out, void* dwg_out,
+                                  void* workspace, size_t ws_bytes, void* stream) {
   if (N < 0 || H <= 0 || E < 1 || E > kMaxE || K < 1 || K > E)
     return fail_arg("moe_router_bwd: bad shape N=%lld H=%lld E=%lld K=%lld", (long long)N, (long long)H,
                     (long long)E, (long long)K);
@@ -2569,6 +2611,13 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
       (gw_dtype != MOE_F32 && gw_dtype != MOE_BF16))
     return fail_arg("moe_router_bwd: unsupported dtype");
   if (!x || !wg || !logits || !idx || !dx_out || !dwg_out) return fail_arg("moe_router_bwd: null pointer argument");
+  if (dx_add != nullptr && N > 0) {
+    // the addend is read while dx is written: the two must not overlap
+    const int64_t nb = N * H * (x_dtype == MOE_BF16 ? 2 : 4);
+    const char* a = static_cast<const char*>(dx_add);
+    const char* d = static_cast<const char*>(dx_out);
+    if (a < d + nb && d < a + nb) return fail_arg("moe_router_bwd: dx_add overlaps dx_out");
+  }
   if (aux_coef != 0.f && !cnt) return fail_arg("moe_router_bwd: aux_coef != 0 needs cnt");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const BwdPlan p = plan_bwd(N > 0 ? N : 1, H, E, x_dtype, wg_dtype);
@@ -2587,6 +2636,8 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
   const bool mfma = p.mfma && aligned16(x) && aligned16(dx_out);
   uint16_t* gb = mfma ? reinterpret_cast<uint16_t*>(ws + p.off_gb) : nullptr;
   int nchunk = p.nchunk;
+  const bool add_fused = dx_add != nullptr && x_dtype == MOE_BF16 && aligned16(dx_add);
+  const uint16_t* addb = add_fused ? static_cast<const uint16_t*>(dx_add) : nullptr;
   if (mfma && p.stream) {
     // streaming form: dL/dlogits is formed inside the dx / dwg kernel, per chunk
     const uint16_t* xb = static_cast<const uint16_t*>(x);
@@ -2594,11 +2645,12 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
     uint16_t* dxb = static_cast<uint16_t*>(dx_out);
 #define MOE_DXDWS(NTEv)                                                                                          \
   launch_dxdw_stream<NTEv>(s, xb, wb, logits, idx, grad_w, gw_dtype, cnt, grad_aux, grad_z, aux_coef, z_coef,    \
-                           (int)N, (int)H, (int)E, (int)K, p.tc_len, p.nchunk, dxb, wsdw)
+                           (int)N, (int)H, (int)E, (int)K, p.tc_len, p.nchunk, dxb, wsdw, nullptr, 0, addb)
     if (p.NTE == 1) MOE_DXDWS(1);
     else MOE_DXDWS(2);
 #undef MOE_DXDWS
     if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+    if (dx_add != nullptr && addb == nullptr) launch_add_rows(s, dx_out, dx_add, N * H, x_dtype);
     launch_reduce(s, wsdw, nchunk, H * E, dwg_out, wg_dtype);
     return check_launch("moe_router_bwd");
   }
@@ -2621,11 +2673,12 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
     const dim3 grid((unsigned)(p.nchunk * nht));
     if (p.EK == 2)
       MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_wide<2, 4>), grid, dim3(256), 0, s, xb, wb, gb, (int)N, (int)H,
-                 (int)E, p.tc_len, nht, dxb, wsdw);
+                 (int)E, p.tc_len, nht, dxb, addb, wsdw);
     else
       MOE_LAUNCH("k_router_dxdw_bf16", (k_router_dxdw_wide<4, 8>), grid, dim3(256), 0, s, xb, wb, gb, (int)N, (int)H,
-                 (int)E, p.tc_len, nht, dxb, wsdw);
+                 (int)E, p.tc_len, nht, dxb, addb, wsdw);
     if (int rc = check_launch("k_router_dxdw_bf16")) return rc;
+    if (dx_add != nullptr && addb == nullptr) launch_add_rows(s, dx_out, dx_add, N * H, x_dtype);
     launch_reduce(s, wsdw, nchunk, H * E, dwg_out, wg_dtype);
     return check_launch("moe_router_bwd");
   }
@@ -2682,8 +2735,19 @@ extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg
                        wsdw);
     if (int rc = check_launch("k_router_dw_generic")) return rc;
   }
+  // the forms above take no addend: dx += dx_add in a separate pass
+  if (dx_add != nullptr) launch_add_rows(s, dx_out, dx_add, N * H, x_dtype);
   const int64_t len = H * E;
   launch_reduce(s,
                      wsdw, nchunk, len, dwg_out, wg_dtype);
   return check_launch("moe_router_bwd");
+}
+
+extern "C" int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg_dtype, const float* logits,
+                              const int64_t* idx, const void* grad_w, int gw_dtype, const int64_t* cnt,
+                              const float* grad_aux, const float* grad_z, float aux_coef, float z_coef, int64_t N,
+                              int64_t H, int64_t E, int64_t K, void* dx_out, void* dwg_out, void* workspace,
+                              size_t ws_bytes, void* stream) {
+  return moe_router_bwd_acc(x, x_dtype, wg, wg_dtype, logits, idx, grad_w, gw_dtype, cnt, grad_aux, grad_z, aux_coef,
+                            z_coef, N, H, E, K, nullptr, dx_out, dwg_out, workspace, ws_bytes, stream);
 }

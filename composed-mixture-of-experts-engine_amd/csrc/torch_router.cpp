@@ -62,8 +62,11 @@ at::Tensor fwd_workspace(size_t nbytes, const at::Device& dev, hipStream_t s) {
 }
 
 struct RouterFn : public torch::autograd::Function<RouterFn> {
+  // link_x: x is also returned, as an eighth output, for the layer's expert path to consume.  Its gradient
+  // (the expert path's gradient of x) then arrives here as an upstream gradient and is added inside the dx
+  // kernel, instead of autograd summing the two contributions to x's gradient in a separate addition.
   static variable_list forward(AutogradContext* ctx, const Variable& x_in, const Variable& gw_in, int64_t k,
-                               double aux_coef, double z_coef, const std::optional<Variable>& bias_in) {
+                               double aux_coef, double z_coef, const std::optional<Variable>& bias_in, bool link_x) {
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(x_in.device());
     const at::Tensor x = x_in.contiguous();
     const at::Tensor gw = gw_in.contiguous();
@@ -104,12 +107,13 @@ struct RouterFn : public torch::autograd::Function<RouterFn> {
     ctx->saved_data["z_coef"] = z_coef;
     ctx->set_materialize_grads(false);
     ctx->mark_non_differentiable({idx, logits, cnt, stats});
+    if (link_x) return {idx, w, aux, z, logits, cnt, stats, x_in};
     return {idx, w, aux, z, logits, cnt, stats};
   }
 
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     const bool need_x = ctx->needs_input_grad(0), need_w = ctx->needs_input_grad(1);
-    variable_list out(6);
+    variable_list out(7);
     if (!(need_x || need_w)) return out;
     const auto saved = ctx->get_saved_variables();
     const at::Tensor& x = saved[0];
@@ -121,6 +125,9 @@ struct RouterFn : public torch::autograd::Function<RouterFn> {
     at::Tensor g_w = grads[1];
     at::Tensor g_aux = grads[2];
     at::Tensor g_z = grads[3];
+    // the linked x output's gradient (the expert path's gradient of x), if any
+    at::Tensor dx_add;
+    if (need_x && grads.size() > 7 && grads[7].defined()) dx_add = grads[7].to(x.scalar_type()).contiguous();
     const float aux_coef = g_aux.defined() ? (float)ctx->saved_data["aux_coef"].toDouble() : 0.f;
     const float z_coef = g_z.defined() ? (float)ctx->saved_data["z_coef"].toDouble() : 0.f;
     int gdt = MOE_F32;
@@ -136,17 +143,19 @@ struct RouterFn : public torch::autograd::Function<RouterFn> {
     at::Tensor dw;
     if (N == 0) {
       dw = at::zeros({H, E}, gw.options());
+      dx.zero_();
     } else {
       dw = at::empty({H, E}, gw.options());
       const int xdt = code_of(x), wdt = code_of(gw);
       const size_t nbytes = moe_router_bwd_workspace(N, H, E, K, xdt, wdt);
       const at::Tensor ws = at::empty({std::max<int64_t>((int64_t)nbytes, 1)}, x.options().dtype(at::kByte));
       const hipStream_t s = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(x.device().index()).stream();
-      const int rc = moe_router_bwd(x.data_ptr(), xdt, gw.data_ptr(), wdt, logits.data_ptr<float>(),
-                                    idx.data_ptr<int64_t>(), g_w.defined() ? g_w.data_ptr() : nullptr, gdt,
-                                    cnt.data_ptr<int64_t>(), g_aux.defined() ? g_aux.data_ptr<float>() : nullptr,
-                                    g_z.defined() ? g_z.data_ptr<float>() : nullptr, aux_coef, z_coef, N, H, E, K,
-                                    dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), nbytes, s);
+      const int rc = moe_router_bwd_acc(x.data_ptr(), xdt, gw.data_ptr(), wdt, logits.data_ptr<float>(),
+                                        idx.data_ptr<int64_t>(), g_w.defined() ? g_w.data_ptr() : nullptr, gdt,
+                                        cnt.data_ptr<int64_t>(), g_aux.defined() ? g_aux.data_ptr<float>() : nullptr,
+                                        g_z.defined() ? g_z.data_ptr<float>() : nullptr, aux_coef, z_coef, N, H, E, K,
+                                        dx_add.defined() ? dx_add.data_ptr() : nullptr, dx.data_ptr(), dw.data_ptr(),
+                                        ws.data_ptr(), nbytes, s);
       if (rc != 0) raise_rc(rc, "moe_router_bwd");
     }
     if (need_x) out[0] = dx;
@@ -156,8 +165,8 @@ struct RouterFn : public torch::autograd::Function<RouterFn> {
 };
 
 variable_list router_core(const at::Tensor& x, const at::Tensor& gate_w, int64_t k, double aux_coef,
-                          double z_coef, const std::optional<at::Tensor>& bias) {
-  return RouterFn::apply(x, gate_w, k, aux_coef, z_coef, bias);
+                          double z_coef, const std::optional<at::Tensor>& bias, bool link_x) {
+  return RouterFn::apply(x, gate_w, k, aux_coef, z_coef, bias, link_x);
 }
 
 }  // namespace
@@ -166,5 +175,5 @@ PYBIND11_MODULE(_moe_torch, m) {
   m.doc() = "Native autograd binding of the fused HIP router (forward and backward over the moe_mi355 C ABI).";
   m.def("router_core", &router_core, "(x, gate_w, k, aux_coef, z_coef, bias) -> (idx, w, aux, z, logits, cnt, stats)",
         pybind11::arg("x"), pybind11::arg("gate_w"), pybind11::arg("k"), pybind11::arg("aux_coef"),
-        pybind11::arg("z_coef"), pybind11::arg("bias") = pybind11::none());
+        pybind11::arg("z_coef"), pybind11::arg("bias") = pybind11::none(), pybind11::arg("link_x") = false);
 }

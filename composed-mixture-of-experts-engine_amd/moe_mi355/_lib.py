@@ -46,6 +46,11 @@ _SIGNATURES = {
         _I32,
         [_P, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _F32, _F32, _I64, _I64, _I64, _I64, _P, _P, _P, _SZ, _P],
     ),
+    "moe_router_bwd_acc": (
+        _I32,
+        [_P, _I32, _P, _I32, _P, _P, _P, _I32, _P, _P, _P, _F32, _F32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ,
+         _P],
+    ),
     "moe_plan_workspace": (_SZ, [_I64, _I64, _I64]),
     "moe_plan": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "moe_plan_noalloc": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P]),

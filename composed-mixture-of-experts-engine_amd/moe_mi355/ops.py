@@ -87,9 +87,12 @@ def router_backward(
     grad_z: Optional[torch.Tensor] = None,
     aux_coef: float = 0.0,
     z_coef: float = 0.0,
+    dx_add: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Fused router backward: returns ``(dx [N,H] x.dtype, dgate_w [H,E] gate_w.dtype)``."""
-    dev = L.require_device(x, gate_w, logits, idx, grad_w, cnt)
+    """Fused router backward: returns ``(dx [N,H] x.dtype, dgate_w [H,E] gate_w.dtype)``; with ``dx_add``
+    ([N, H], x's dtype) dx is the router's gradient of x plus dx_add, summed inside the dx kernel
+    (moe_router_bwd_acc)."""
+    dev = L.require_device(x, gate_w, logits, idx, grad_w, cnt, dx_add)
     x = x.contiguous()
     gate_w = gate_w.contiguous()
     logits = logits.contiguous()
@@ -115,12 +118,23 @@ def router_backward(
     dw = torch.empty((H, E), dtype=gate_w.dtype, device=dev)
     nbytes = lib.moe_router_bwd_workspace(N, H, E, K, xdt, wdt)
     ws = L.workspace(nbytes, dev)
-    rc = lib.moe_router_bwd(
-        x.data_ptr(), xdt, gate_w.data_ptr(), wdt, logits.data_ptr(), idx.data_ptr(),
-        L.ptr(grad_w), gdt, L.ptr(cnt), L.ptr(grad_aux), L.ptr(grad_z),
-        float(aux_coef), float(z_coef), N, H, E, K,
-        dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
-    )
+    if dx_add is None:
+        rc = lib.moe_router_bwd(
+            x.data_ptr(), xdt, gate_w.data_ptr(), wdt, logits.data_ptr(), idx.data_ptr(),
+            L.ptr(grad_w), gdt, L.ptr(cnt), L.ptr(grad_aux), L.ptr(grad_z),
+            float(aux_coef), float(z_coef), N, H, E, K,
+            dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+        )
+    else:
+        if dx_add.shape != (N, H) or dx_add.dtype != x.dtype:
+            raise ValueError(f"router_backward: dx_add must be [{N}, {H}] {x.dtype}")
+        dx_add = dx_add.contiguous()
+        rc = lib.moe_router_bwd_acc(
+            x.data_ptr(), xdt, gate_w.data_ptr(), wdt, logits.data_ptr(), idx.data_ptr(),
+            L.ptr(grad_w), gdt, L.ptr(cnt), L.ptr(grad_aux), L.ptr(grad_z),
+            float(aux_coef), float(z_coef), N, H, E, K,
+            dx_add.data_ptr(), dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+        )
     L.check(rc, "moe_router_bwd")
     return dx, dw
 

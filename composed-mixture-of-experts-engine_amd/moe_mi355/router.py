@@ -63,7 +63,12 @@ class RouterCore:
     to k, the coefficients or the bias.  The checks below raise the errors the ctypes path raises."""
 
     @staticmethod
-    def apply(x, gate_w, k: int, aux_coef: float, z_coef: float, bias: Optional[torch.Tensor] = None):
+    def apply(x, gate_w, k: int, aux_coef: float, z_coef: float, bias: Optional[torch.Tensor] = None,
+              link_x: bool = False):
+        """``link_x``: also return x itself as an eighth output.  A caller that feeds that output (rather than
+        x) to its other consumer of the tokens hands that consumer's gradient of x to this Function's backward,
+        which adds it inside the dx kernel (moe_router_bwd_acc) instead of autograd summing the two
+        contributions to x's gradient in a separate addition."""
         L.require_device(x, gate_w, bias)
         N, H = x.shape
         H2, E = gate_w.shape
@@ -71,7 +76,7 @@ class RouterCore:
             raise ValueError(f"router_forward: hidden dims differ ({H} vs {H2})")
         L.dtype_code(x.dtype)
         L.dtype_code(gate_w.dtype)
-        return tuple(_binding().router_core(x, gate_w, int(k), float(aux_coef), float(z_coef), bias))
+        return tuple(_binding().router_core(x, gate_w, int(k), float(aux_coef), float(z_coef), bias, bool(link_x)))
 
 
 def route(x: torch.Tensor, gate_w: torch.Tensor, k: int, aux_coef: float = 0.0, z_coef: float = 0.0,

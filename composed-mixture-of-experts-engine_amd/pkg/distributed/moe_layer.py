@@ -260,9 +260,23 @@ class DistributedMoELayer(nn.Module):
             raise ValueError(f"tokens must be rank 2 or 3, got {tokens.dim()}")
         H = tokens.shape[-1]
         flat = tokens.reshape(-1, H)
-        with self._deferred_router_check():
+        with self._deferred_router_check(), self._linked_tokens():
             idx, weights, _cnt = self.router(flat)
-        return self._experts_forward(flat, idx, weights).reshape(original_shape)
+        # the router hands the tokens back as a linked output (a view of the same memory): the expert path's
+        # gradient of the tokens then reaches the router's backward, which adds it inside its dx kernel, so
+        # x's gradient is formed in one pass instead of autograd adding the two paths' gradients afterwards
+        # (the reference's autograd sums them, moe_layer.py L:288 and L:317-319)
+        linked = self.router.take_linked_tokens()
+        return self._experts_forward(flat if linked is None else linked, idx, weights).reshape(original_shape)
+
+    @contextlib.contextmanager
+    def _linked_tokens(self):
+        r = self.router
+        r._link_x = isinstance(r, MoERouter) and r.bias is None
+        try:
+            yield
+        finally:
+            r._link_x = False
 
     @contextlib.contextmanager
     def _deferred_router_check(self):

@@ -240,6 +240,10 @@ class MoERouter(torch.nn.Module):
         # set by a caller that enqueues more GPU work after the routing and runs the checks itself at its next
         # synchronisation (check_pending): the forward then does not stop the stream mid-way
         self._defer_check = False
+        # set by DistributedMoELayer around its call: the forward also returns the tokens as a linked output
+        # (take_linked_tokens) whose gradient the router's backward adds into its own gradient of the tokens
+        self._link_x = False
+        self._x_link: Optional[torch.Tensor] = None
         self._last_logits: Optional[torch.Tensor] = None
         self.last_aux_loss: Optional[torch.Tensor] = None
         self.last_z_loss: Optional[torch.Tensor] = None
@@ -275,12 +279,22 @@ class MoERouter(torch.nn.Module):
             _no_reference_path()
 
         timing = _LaunchTiming.start(flat)
-        idx, w, aux, z, logits, cnt, stats = RouterCore.apply(
-            flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, self._logit_bias()
+        outs = RouterCore.apply(
+            flat, self.gate_w, self.top_k, self.aux_loss_coef, self.z_loss_coef, self._logit_bias(),
+            link_x=self._link_x,
         )
+        idx, w, aux, z, logits, cnt, stats = outs[:7]
+        # with _link_x (set by DistributedMoELayer around its call) the tokens come back as an eighth output for
+        # the expert path, so its gradient of the tokens is summed inside the router's dx kernel
+        self._x_link = outs[7] if self._link_x else None
         if timing is not None:
             timing.stop()
         return self._finish(flat, idx, w, aux, z, logits, cnt, stats, timing)
+
+    def take_linked_tokens(self) -> Optional[torch.Tensor]:
+        """The tokens of the last forward made with ``_link_x`` set, as the router's linked output (once)."""
+        x, self._x_link = self._x_link, None
+        return x
 
     def forward_with_norm(self, tokens: torch.Tensor, norm_weight: torch.Tensor, eps: float):
         """Route ``rmsnorm(tokens)`` with the norm fused into the router's read of ``tokens``

@@ -142,6 +142,19 @@ int moe_router_bwd(const void* x, int x_dtype, const void* wg, int wg_dtype,
                    int64_t N, int64_t H, int64_t E, int64_t K,
                    void* dx_out, void* dwg_out,
                    void* workspace, size_t ws_bytes, void* stream);
+/* The router backward with the rest of x's gradient folded in: dx_out = G @ wg^T + dx_add, where dx_add
+ * [N, H] (x_dtype, must not overlap dx_out) is the gradient of x from the layer's other consumer of the
+ * tokens, the expert path.  In the reference autograd sums the two contributions to x.grad, the router's
+ * (moe_router.py L:545-546) and the dispatch's (moe_layer.py L:317-319 via index/repeat_interleave), in a
+ * separate addition; here the sum is formed in the dx stores (bf16: both rounded values added in fp32 and
+ * rounded once, as that addition does).  Otherwise identical to moe_router_bwd. */
+int moe_router_bwd_acc(const void* x, int x_dtype, const void* wg, int wg_dtype,
+                       const float* logits, const int64_t* idx, const void* grad_w, int gw_dtype,
+                       const int64_t* cnt, const float* grad_aux, const float* grad_z,
+                       float aux_coef, float z_coef,
+                       int64_t N, int64_t H, int64_t E, int64_t K,
+                       const void* dx_add, void* dx_out, void* dwg_out,
+                       void* workspace, size_t ws_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Dispatch planner.  From the router's idx [N, K] (int64) builds, on the

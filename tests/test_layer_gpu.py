@@ -185,3 +185,35 @@ def test_layer_checks_run_at_the_end_of_the_forward():
     assert not layer.router._defer_check
     with pytest.raises(AssertionError, match="NaN in expert indices"):
         layer.router(x)
+
+
+@pytest.mark.parametrize("case", [(256, 128, 8, 2, "reference", False), (512, 256, 64, 6, "routed", True),
+                                  (256, 128, 16, 4, "routed", False)],
+                         ids=lambda c: f"H{c[0]}-F{c[1]}-E{c[2]}-K{c[3]}-{c[4]}-{'aux' if c[5] else 'plain'}")
+def test_layer_linked_tokens_gradient(case, monkeypatch):
+    """The layer hands the expert path's gradient of the tokens to the router's backward, which adds it inside
+    its dx kernel: x.grad (and every other gradient) bit-identical to the same layer with the two gradients
+    summed by autograd (the router's tokens link switched off)."""
+    H, Fd, E, K, layout, losses = case
+    say(f"[layer linked tokens] {case}")
+    aux, z = (0.01, 1e-3) if losses else (0.0, 0.0)
+    g = torch.Generator().manual_seed(5)
+    N = 777
+    x = torch.randn(N, H, generator=g).to(torch.bfloat16).to(dev())
+    gout = torch.randn(N, H, generator=g).to(torch.bfloat16).to(dev())
+    grads = []
+    for linked in (True, False):
+        layer = _layer(H, Fd, E, K, torch.bfloat16, layout=layout, aux=aux, z=z, seed=3)
+        if not linked:
+            monkeypatch.setattr(type(layer.router), "take_linked_tokens", lambda self: None)
+        xd = x.clone().requires_grad_(True)
+        out = layer(xd)
+        loss = (out.float() * gout.float()).sum()
+        if losses:
+            loss = loss + layer.router.last_aux_loss + layer.router.last_z_loss
+        loss.backward()
+        torch.cuda.synchronize()
+        grads.append([xd.grad, layer.router.gate_w.grad, layer.w_gate.grad, layer.w_up.grad, layer.w_down.grad])
+        monkeypatch.undo()
+    for what, a, b in zip(("dx", "dgate_w", "dw_gate", "dw_up", "dw_down"), *grads):
+        assert torch.equal(a, b), f"{what} differs between the linked and the autograd-summed token gradients"

@@ -303,3 +303,38 @@ def test_router_nan_gate_column_is_never_picked(N, H, E, K, dt):
     assert ok.float().mean() > 0.9
     assert torch.equal(idx[ok], ref["idx"][ok])
     assert_rel(wt[ok], ref["w"][ok], TOL[dt], "weights")
+
+
+# (N, H, E, K, x dtype, gate dtype): the streaming backward (16- and 4-wave), the wide backward, the
+# non-streaming MFMA form, the fp32 and the generic forms (the last three add the addend in a separate pass)
+ACC_SHAPES = [
+    (16384, 4096, 8, 2, torch.bfloat16, torch.bfloat16),
+    (300, 512, 8, 2, torch.bfloat16, torch.bfloat16),
+    (1000, 256, 16, 4, torch.bfloat16, torch.bfloat16),
+    (8192, 2048, 128, 8, torch.bfloat16, torch.bfloat16),
+    (129, 320, 48, 5, torch.bfloat16, torch.bfloat16),
+    (96, 96, 64, 4, torch.bfloat16, torch.bfloat16),
+    (4096, 512, 8, 2, torch.float32, torch.float32),
+    (50, 72, 8, 2, torch.bfloat16, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("shape", ACC_SHAPES, ids=_ids)
+def test_router_bwd_acc_adds_the_other_gradient(shape):
+    """moe_router_bwd_acc: dx = the router's gradient of x + dx_add, formed inside the dx kernel, bit-identical
+    to moe_router_bwd's dx followed by the tensor addition autograd would make (bf16: each rounded value
+    widened, summed in fp32, rounded once); dwg unchanged."""
+    N, H, E, K, xdt, wdt = shape
+    say(f"[router bwd acc] N={N} H={H} E={E} K={K} {xdt} {wdt}")
+    d = dev()
+    g = torch.Generator().manual_seed(N + H + E)
+    x = torch.randn(N, H, generator=g).to(xdt).to(d)
+    w = (torch.randn(H, E, generator=g) * 0.05).to(wdt).to(d)
+    gw = torch.randn(N, K, generator=g).to(d)
+    add = torch.randn(N, H, generator=g).to(xdt).to(d)
+    idx, _wt, logits, _lse, cnt, _stats = ops.router_forward(x, w, K)
+    dx0, dw0 = ops.router_backward(x, w, logits, idx, gw, cnt, aux_coef=0.01, z_coef=1e-3)
+    dx1, dw1 = ops.router_backward(x, w, logits, idx, gw, cnt, aux_coef=0.01, z_coef=1e-3, dx_add=add)
+    torch.cuda.synchronize()
+    assert torch.equal(dx1, dx0 + add), "dx differs from dx + dx_add"
+    assert torch.equal(dw1, dw0)
