@@ -54,6 +54,8 @@ _SIGNATURES = {
     "moe_plan_workspace": (_SZ, [_I64, _I64, _I64]),
     "moe_plan": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "moe_plan_noalloc": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P]),
+    "moe_cumcount_workspace": (_SZ, [_I64]),
+    "moe_cumcount": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "moe_permute": (_I32, [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _P]),
     "moe_combine": (_I32, [_P, _I32, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "moe_combine_bwd": (_I32, [_P, _P, _I32, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P]),

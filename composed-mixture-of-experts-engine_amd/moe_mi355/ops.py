@@ -329,6 +329,25 @@ class Plan:
         return None if self.drop is None else self.drop.view(torch.uint8)
 
 
+def cumcount(groups: torch.Tensor) -> torch.Tensor:
+    """Each element's 0-based position among the earlier elements of its group, for any int64 group ids
+    (moe_cumcount: stable radix sort of the ids, ranks from the sorted positions)."""
+    dev = L.require_device(groups)
+    g = groups.reshape(-1).contiguous()
+    if g.dtype != torch.int64:
+        g = g.long()
+    n = g.numel()
+    out = torch.empty(n, dtype=torch.int64, device=dev)
+    if n == 0:
+        return out
+    lib = L.load()
+    nbytes = lib.moe_cumcount_workspace(n)
+    ws = L.workspace(nbytes, dev)
+    rc = lib.moe_cumcount(g.data_ptr(), n, out.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev))
+    L.check(rc, "moe_cumcount")
+    return out
+
+
 def plan(idx: torch.Tensor, num_experts: int, capacity: int = -1, layout: int = LAYOUT_REFERENCE) -> Plan:
     """Build the dispatch plan from the router's top-k indices (no host sync)."""
     dev = L.require_device(idx)

@@ -78,16 +78,24 @@ class _ExpertTimer:
         return max(float(self.a.elapsed_time(self.b)), 0.0)
 
 
-def _cumcount(groups: torch.Tensor) -> torch.Tensor:
-    """Each element's 0-based position among earlier elements of its group (L:64-115).
+# The planner's key tables hold one contiguous range of at most this many ids (and K * E <= 8192 keys).
+_PLAN_MAX_KEYS = 1024
 
-    Runs the planner's stable-grouping kernel (one column of K=1)."""
+
+def _cumcount(groups: torch.Tensor) -> torch.Tensor:
+    """Each element's 0-based position among earlier elements of its group (L:64-115), for any integer ids.
+
+    Ids spanning at most 1024 values run the planner's stable-grouping kernel (one column of K=1); wider
+    ranges run moe_cumcount (a stable radix sort of the ids).  One host read of the id range."""
     n = groups.shape[0]
     if n == 0:
         return torch.empty(0, dtype=torch.long, device=groups.device)
     g = groups.reshape(n, 1).long()
-    g = g - g.min()
-    E = int(g.max().item()) + 1
+    lo, hi = (int(v) for v in torch.stack([g.min(), g.max()]).tolist())
+    if hi - lo + 1 > _PLAN_MAX_KEYS:
+        return ops.cumcount(g.reshape(-1))
+    g = g - lo
+    E = hi - lo + 1
     # rank of each element within its key = position in the stable sort minus the key's offset
     p = ops.plan(g, max(E, 1), capacity=-1, layout=ops.LAYOUT_ROUTED)
     pos = p.slot_row.long()
@@ -95,19 +103,21 @@ def _cumcount(groups: torch.Tensor) -> torch.Tensor:
 
 
 def compute_capacity_drop_mask(idx: torch.Tensor, num_experts: int, capacity: int) -> torch.Tensor:
-    """``drop[t, k] = cumcount(idx[:, k])[t] >= capacity`` per column (L:118-155)."""
+    """``drop[t, k] = cumcount(idx[:, k])[t] >= capacity`` per column (L:118-155), for any integer ids."""
     N, K = idx.shape
     if N == 0:
         return torch.zeros(N, K, dtype=torch.bool, device=idx.device)
+    if capacity < 0:  # every slot is at a position >= capacity
+        return torch.ones(N, K, dtype=torch.bool, device=idx.device)
     # any integer group ids are valid here, as in the reference (one host read of the range)
     lo, hi = (int(v) for v in torch.stack([idx.min(), idx.max()]).tolist())
     if lo < 0 or hi >= num_experts:
         idx = idx - lo
         num_experts = hi - lo + 1
-    # capacity < 0 drops every slot (position >= capacity always holds)
-    p = ops.plan(idx, num_experts, capacity=max(int(capacity), 0), layout=ops.LAYOUT_REFERENCE)
-    if capacity < 0:
-        return torch.ones(N, K, dtype=torch.bool, device=idx.device)
+    if num_experts > _PLAN_MAX_KEYS or K * num_experts > 8192 or K > num_experts:
+        # ids too many for the planner's key tables: the column ranks from the general kernel
+        return torch.stack([_cumcount(idx[:, k]) >= capacity for k in range(K)], dim=1)
+    p = ops.plan(idx, num_experts, capacity=int(capacity), layout=ops.LAYOUT_REFERENCE)
     return p.drop
 
 

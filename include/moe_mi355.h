@@ -197,6 +197,15 @@ int moe_plan_noalloc(const int64_t* idx, int64_t N, int64_t K, int64_t E, int64_
                      uint8_t* drop_out, int32_t* row_slot, int32_t* slot_row, int32_t* offsets, int32_t* ndrop,
                      void* stream);
 
+/* _cumcount for any int64 group ids (pkg/distributed/moe_layer.py L:64-115): out[i] = the number of j < i
+ * with groups[j] == groups[i].  moe_plan computes the same for ids that fit its key tables (one contiguous
+ * range of at most 1024 values); this entry point takes every other input (any range, any number of distinct
+ * ids, negative ids): a stable radix sort of (id, position) pairs (rocPRIM), each element's rank being its
+ * sorted position minus the first sorted position of its id.  n <= 2^31 - 1.  Not for graph capture (the sort
+ * clears its counters with hipMemsetAsync). */
+size_t moe_cumcount_workspace(int64_t n);
+int moe_cumcount(const int64_t* groups, int64_t n, int64_t* out, void* workspace, size_t ws_bytes, void* stream);
+
 /* Permute (dispatch): xp[slot_row[t*K+k]] = x[t] for every slot whose row is computed (0 <= row <
  * offsets[E]); other rows of xp are left unwritten.  Rows are row_bytes long (a multiple of 16); each token
  * row is read once and written to its K rows.  Replaces flat[sort_order].repeat_interleave(K)

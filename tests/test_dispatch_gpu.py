@@ -100,6 +100,34 @@ def test_cumcount_and_drop_mask_golden_vectors():
     assert compute_capacity_drop_mask(torch.tensor([[0], [1], [0], [1]], device=d), 2, 0).all()
 
 
+WIDE_IDS = [
+    ("span_1e6", 200000, lambda g, n: torch.randint(0, 1_000_001, (n,), generator=g)),
+    ("few_ids_wide_span", 50000, lambda g, n: torch.tensor([-7, 10**6, 3, 2**40])[torch.randint(0, 4, (n,), generator=g)]),
+    ("negative", 30000, lambda g, n: torch.randint(-(2**50), 2**50, (n,), generator=g)),
+    ("all_distinct", 4097, lambda g, n: torch.randperm(n, generator=g) * 1000 - 5),
+    ("one_element", 1, lambda g, n: torch.tensor([123456789])),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_IDS, ids=lambda c: c[0])
+def test_cumcount_any_integer_ids(case):
+    """_cumcount on id ranges wider than the planner's keys (moe_cumcount: stable radix sort + ranks) against
+    the integer oracle (oracle/plan.py cumcount), bit-exact; and the per-column drop mask on such ids."""
+    from pkg.distributed.moe_layer import _cumcount, compute_capacity_drop_mask
+
+    name, n, make = case
+    say(f"[cumcount wide ids] {name} n={n}")
+    g = torch.Generator().manual_seed(n)
+    ids = make(g, n).long()
+    got = _cumcount(ids.to(dev())).cpu().numpy()
+    assert np.array_equal(got, OP.cumcount(ids.numpy()))
+    if n >= 2:
+        cols = torch.stack([ids, ids.flip(0)], dim=1)
+        cap = max(1, int(np.bincount(OP.cumcount(ids.numpy())).size // 2))
+        m = compute_capacity_drop_mask(cols.to(dev()), 8, cap).cpu().numpy()
+        assert np.array_equal(m, OP.drop_mask(cols.numpy(), cap))
+
+
 def _rows_and_y(N, K, E, H, dt, seed, cap, layout):
     idx = _idx(N, K, E, seed)
     g = torch.Generator().manual_seed(seed + 1)
