@@ -346,16 +346,17 @@ def gemm_flops(R, H, F):
             "k_gemm_swiglu_dwd": 2 * R * H * F, "k_gemm_swiglu_dw1": 2 * R * 2 * F * H}
 
 
-def layer_hbm_bytes(N, H, E, K, R):
+def layer_hbm_bytes(N, H, E, K, R, es=2):
     """Algorithmic HBM bytes per launch of the layer's data-movement and router kernels (bf16 rows, R computed
     rows): each token row is read once by the permute and written to its rows; the combine reads the rows and
     writes the tokens; the backward passes mirror them."""
-    return {"k_permute": N * H * 2 + R * H * 2 + N * K * 4,
-            "k_combine": R * H * 2 + N * H * 2 + N * K * (2 + 4 + 1),
-            "k_combine_bwd": N * H * 2 + 2 * R * H * 2 + N * K * (2 + 4 + 1 + 2),
-            "k_unpermute_sum": R * H * 2 + N * H * 2 + N * K * 4,
-            "k_router_fwd_bf16": N * H * 2 + H * E * 2 + N * E * 4 + N * 4 + N * K * (8 + 2),
-            "k_router_dxdw_bf16": 2 * N * H * 2 + N * E * 2 + H * E * 2}
+    return {"k_permute": N * H * es + R * H * es + N * K * 4,
+            "k_combine": R * H * es + N * H * es + N * K * (2 + 4 + 1),
+            "k_combine_bwd": N * H * es + 2 * R * H * es + N * K * (2 + 4 + 1 + 2),
+            "k_unpermute_sum": R * H * es + N * H * es + N * K * 4,
+            "k_router_fwd_bf16": N * H * es + H * E * es + N * E * 4 + N * 4 + N * K * (8 + es),
+            # read x and the expert path's gradient of x (added in the dx stores), write dx
+            "k_router_dxdw_bf16": 3 * N * H * es + N * E * 2 + H * E * es}
 
 
 def build_layer(cfg, torch, inp, layout):
@@ -364,7 +365,7 @@ def build_layer(cfg, torch, inp, layout):
 
     dev = torch.device("cuda:0")
     layer = DistributedMoELayer(cfg.H, cfg.F, cfg.E, cfg.K, build_topology(), capacity_factor=cfg.capacity_factor,
-                                capacity_dropping=cfg.capacity_dropping, dtype=torch.bfloat16, layout=layout,
+                                capacity_dropping=cfg.capacity_dropping, dtype=cfg.dtype, layout=layout,
                                 aux_loss_coef=cfg.aux_coef, z_loss_coef=cfg.z_coef, check_numerics=False).to(dev)
     with torch.no_grad():
         layer.router.gate_w.copy_(inp["gate_w"])
@@ -376,11 +377,18 @@ def build_layer(cfg, torch, inp, layout):
     return layer
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
 def run_layer(args, torch, cfg, layout, inp, default_numerics=False):
+    """Layer fwd+bwd at ``cfg`` (its dtype: bf16, or fp32 with the inputs widened from ``inp``)."""
     dev = torch.device("cuda:0")
     layer = build_layer(cfg, torch, inp, layout)
-    x = inp["x"].to(dev).requires_grad_(True)
-    gout = inp["grad_out"].to(dev)
+    x = inp["x"].to(dev).to(cfg.dtype).requires_grad_(True)
+    gout = inp["grad_out"].to(dev).to(cfg.dtype)
+    peak = MFMA_F32_PEAK_TFLOPS if cfg.dtype == torch.float32 else MFMA_BF16_PEAK_TFLOPS
+    if cfg.dtype == torch.float32:  # ~17 TFLOP of fp32 MFMA per C4 step: a few steps suffice
+        args = argparse.Namespace(**{**vars(args), "steps": min(args.steps, 5), "warmup": min(args.warmup, 1)})
     params = [x, layer.router.gate_w, layer.w_gate, layer.w_up, layer.w_down]
     use_losses = cfg.aux_coef != 0.0 or cfg.z_coef != 0.0
     one = torch.ones((), device=dev)
@@ -407,8 +415,10 @@ def run_layer(args, torch, cfg, layout, inp, default_numerics=False):
         layer.check_numerics = False
         layer.router.sync_profile = False
     fl = gemm_flops(R, cfg.H, cfg.F)
+    if cfg.dtype == torch.float32:
+        fl = {k + "_f32": v for k, v in fl.items()}
     kernels = kernel_table(prof, fl, 1e12, "TFLOPs")
-    hbm = layer_hbm_bytes(cfg.T, cfg.H, cfg.E, cfg.K, R)
+    hbm = layer_hbm_bytes(cfg.T, cfg.H, cfg.E, cfg.K, R, es=4 if cfg.dtype == torch.float32 else 2)
     for name, ent in kernel_table(prof, hbm, 1e9, "GBps").items():
         if name in hbm:
             kernels[name].update(ent)
@@ -416,7 +426,7 @@ def run_layer(args, torch, cfg, layout, inp, default_numerics=False):
     dom = max((k for k in kernels if k in fl), key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
     achieved = kernels[dom]["TFLOPs"]
     step_flops = 18 * R * cfg.H * cfg.F
-    gemm_ms = sum(prof[k][1] / prof[k][0] for k in GEMM_KERNELS if k in prof)
+    gemm_ms = sum(prof[k][1] / prof[k][0] for k in fl if k in prof)
     res = {
         "workload": f"{cfg.name} layer fwd+bwd ({layout} layout)", "tokens": cfg.T, "d_model": cfg.H,
         "experts": cfg.E, "ffn": cfg.F, "top_k": cfg.K, "rows_computed": R,
@@ -426,11 +436,11 @@ def run_layer(args, torch, cfg, layout, inp, default_numerics=False):
         "last_expert_compute_ms": round(expert_ms, 4),
         "expert_TFLOP_per_step": step_flops / 1e12,
         "step_TFLOPs": round(step_flops / (ms * 1e-3) / 1e12, 2),
-        "step_frac_of_mfma_peak": round(step_flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "step_frac_of_mfma_peak": round(step_flops / (ms * 1e-3) / 1e12 / peak, 4),
         "gemm_ms_per_step": round(gemm_ms, 4),
         "gemm_TFLOPs": round(step_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else None,
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(dom, f"{cfg.name}:{layout}"),
                      "flops_per_launch": fl[dom], "avg_us": kernels[dom]["avg_us"]},
         "kernels": kernels,
@@ -752,7 +762,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="layer", choices=["layer", "c4", "router", "c1", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
+    ap.add_argument("--workload", default="layer", choices=["layer", "c4", "c4_f32", "router", "c1", "norm_router", "dispatch", "skewed", "fp8_fwd", "all"])
     ap.add_argument("--layout", default="reference", choices=["reference", "routed"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -787,6 +797,8 @@ def main():
         log(f"[bench] C1 router: {extra['c1']['ms_mean']:.4f} ms/step")
         extra["norm_router"] = run_norm_router(args, torch)
         log(f"[bench] norm_router: {extra['norm_router']['ms_per_step']:.4f} ms/step")
+        extra["c4_f32"] = run_layer(args, torch, configs.C4_F32, args.layout, inp)
+        log(f"[bench] C4 layer in fp32: {extra['c4_f32']['ms_per_step']:.2f} ms/step")
         extra["fp8_fwd"] = run_fp8_fwd(args, torch, inp)
         add_mfma_ceiling(extra["fp8_fwd"]["roofline"], extra["fp8_fwd"], fp8=True)
         log(f"[bench] fp8 forward: {extra['fp8_fwd']['fp8_ms_per_step']:.3f} ms/step "
@@ -824,6 +836,12 @@ def main():
         add_mfma_ceiling(roof, extra, fp8=False)
         config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
         config["layout"] = args.layout
+    elif args.workload == "c4_f32":
+        main_res = run_layer(args, torch, configs.C4_F32, args.layout, configs.layer_inputs(configs.C4))
+        cpu = None
+        value, unit, ms = main_res["tokens_per_s"], "tokens/s", main_res["ms_per_step"]
+        roof = main_res.pop("roofline")
+        config = {k: main_res.pop(k) for k in ("workload", "tokens", "d_model", "experts", "ffn", "top_k")}
     elif args.workload == "router":
         main_res = run_router(args, torch)
         add_hbm_ceiling_router(main_res)
@@ -869,7 +887,7 @@ def main():
     out = {
         "metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": {"fp8_fwd": "fp8-e4m3", "c1": "f32"}.get(args.workload, "bf16"),
+        "dtype": {"fp8_fwd": "fp8-e4m3", "c1": "f32", "c4_f32": "f32"}.get(args.workload, "bf16"),
         "data": "synthetic (seeded randn of the BASELINE config shapes; random-init weights)", "config": config,
         "roofline": roof, "cpu_baseline": cpu,
     }

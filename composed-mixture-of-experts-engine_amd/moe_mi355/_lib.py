@@ -84,6 +84,12 @@ _SIGNATURES = {
     "moe_telemetry_fields": (_I32, []),
     "moe_telemetry_record": (_I32, [_P, _I64, _I64, _I64, _F32, _P, _I64, _P, _I64, _P]),
     "moe_swiglu_workspace": (_SZ, [_I64]),
+    "moe_swiglu_f32_workspace": (_SZ, [_I64]),
+    "moe_swiglu_fwd_f32": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "moe_swiglu_bwd_f32": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
     "moe_swiglu_fwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "moe_swiglu_bwd": (
         _I32,

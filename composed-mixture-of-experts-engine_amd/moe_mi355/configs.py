@@ -46,6 +46,8 @@ C1 = Config("C1_router_fp32", T=4096, H=512, E=8, K=2, seed=0, dtype=torch.float
 C2 = Config("C2_router_bf16", T=16384, H=4096, E=8, K=2, seed=1)
 C3 = Config("C3_dispatch_bf16", T=65536, H=2048, E=64, K=6, seed=2, capacity_dropping=True)
 C4 = Config("C4_layer_bf16", T=8192, H=4096, E=8, K=2, F=14336, seed=3)
+# C4 in the reference module's default dtype (float32 tokens, gate and experts), inputs widened from C4's draws
+C4_F32 = Config("C4_layer_fp32", T=8192, H=4096, E=8, K=2, F=14336, seed=3, dtype=torch.float32)
 C5 = Config("C5_skewed_layer_bf16", T=32768, H=2048, E=128, K=8, F=768, seed=4, capacity_factor=1.0,
             capacity_dropping=True, aux_coef=0.01, z_coef=1e-3, zipf_bias=True)
 

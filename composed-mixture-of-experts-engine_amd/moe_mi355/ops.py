@@ -438,27 +438,33 @@ def unpermute_sum(dxp: torch.Tensor, p: Plan, addend: Optional[torch.Tensor] = N
 # ---------------------------------------------------------------------------
 def swiglu_forward(xp: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
                    offsets: torch.Tensor, keep_preact: bool = True):
-    """xp [R,H]; w_gate/w_up [E,F,H]; w_down [E,H,F] (bf16, contiguous) -> (act [R,F], hgu [R,2F], y [R,H]).
-    ``keep_preact=False`` (no backward follows) skips storing the pre-activations: hgu is None."""
+    """xp [R,H]; w_gate/w_up [E,F,H]; w_down [E,H,F] (all bf16 or all fp32, contiguous) -> (act [R,F], hgu [R,2F],
+    y [R,H]).  ``keep_preact=False`` (no backward follows) skips storing the pre-activations: hgu is None."""
     dev = L.require_device(xp, w_gate, w_up, w_down, offsets)
-    for t in (xp, w_gate, w_up, w_down):
-        if t.dtype != torch.bfloat16:
-            raise TypeError("swiglu_forward: the grouped GEMM runs on bfloat16 tensors")
-        if not t.is_contiguous():
-            raise ValueError("swiglu_forward: tensors must be contiguous")
+    f32 = _gemm_dtype_is_f32("swiglu_forward", xp, w_gate, w_up, w_down)
     R, H = xp.shape
     E, F, _ = w_gate.shape
     act = torch.empty((R, F), dtype=xp.dtype, device=dev)
     hgu = torch.empty((R, 2 * F), dtype=xp.dtype, device=dev) if keep_preact else None
     y = torch.empty((R, H), dtype=xp.dtype, device=dev)
     lib = L.load()
-    nbytes = lib.moe_swiglu_workspace(E)
+    nbytes = lib.moe_swiglu_f32_workspace(E) if f32 else lib.moe_swiglu_workspace(E)
     ws = L.workspace(nbytes, dev)
-    rc = lib.moe_swiglu_fwd(xp.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(),
-                            offsets.data_ptr(), R, H, F, E, act.data_ptr(), L.ptr(hgu), y.data_ptr(),
-                            ws.data_ptr(), nbytes, L.stream_of(dev))
-    L.check(rc, "moe_swiglu_fwd")
+    fn = lib.moe_swiglu_fwd_f32 if f32 else lib.moe_swiglu_fwd
+    rc = fn(xp.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), offsets.data_ptr(), R, H, F, E,
+            act.data_ptr(), L.ptr(hgu), y.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev))
+    L.check(rc, "moe_swiglu_fwd_f32" if f32 else "moe_swiglu_fwd")
     return act, hgu, y
+
+
+def _gemm_dtype_is_f32(what, *ts) -> bool:
+    """The grouped GEMM runs on all-bf16 (moe_swiglu_*) or all-fp32 (moe_swiglu_*_f32) contiguous tensors."""
+    dt = ts[0].dtype
+    if dt not in (torch.bfloat16, torch.float32) or any(t.dtype != dt for t in ts):
+        raise TypeError(f"{what}: the grouped GEMM runs on all-bfloat16 or all-float32 tensors")
+    if not all(t.is_contiguous() for t in ts):
+        raise ValueError(f"{what}: tensors must be contiguous")
+    return dt == torch.float32
 
 
 # ---------------------------------------------------------------------------
@@ -529,6 +535,8 @@ def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, ke
 def swiglu_backward(dy, xp, act, hgu, w_gate, w_up, w_down, offsets):
     """-> (dxp [R,H], dw_gate [E,F,H], dw_up [E,F,H], dw_down [E,H,F])."""
     dev = L.require_device(dy, xp, act, hgu, w_gate, w_up, w_down, offsets)
+    dy = dy.contiguous()
+    f32 = _gemm_dtype_is_f32("swiglu_backward", dy, xp, act, hgu, w_gate, w_up, w_down)
     R, H = xp.shape
     E, F, _ = w_gate.shape
     dh = torch.empty((R, 2 * F), dtype=xp.dtype, device=dev)
@@ -537,11 +545,11 @@ def swiglu_backward(dy, xp, act, hgu, w_gate, w_up, w_down, offsets):
     dwu = torch.empty_like(w_up)
     dwd = torch.empty_like(w_down)
     lib = L.load()
-    nbytes = lib.moe_swiglu_workspace(E)
+    nbytes = lib.moe_swiglu_f32_workspace(E) if f32 else lib.moe_swiglu_workspace(E)
     ws = L.workspace(nbytes, dev)
-    rc = lib.moe_swiglu_bwd(dy.contiguous().data_ptr(), xp.data_ptr(), act.data_ptr(), hgu.data_ptr(),
-                            w_gate.data_ptr(), w_up.data_ptr(), w_down.data_ptr(), offsets.data_ptr(), R, H, F, E,
-                            dh.data_ptr(), dxp.data_ptr(), dwg.data_ptr(), dwu.data_ptr(), dwd.data_ptr(),
-                            ws.data_ptr(), nbytes, L.stream_of(dev))
-    L.check(rc, "moe_swiglu_bwd")
+    fn = lib.moe_swiglu_bwd_f32 if f32 else lib.moe_swiglu_bwd
+    rc = fn(dy.data_ptr(), xp.data_ptr(), act.data_ptr(), hgu.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(),
+            w_down.data_ptr(), offsets.data_ptr(), R, H, F, E, dh.data_ptr(), dxp.data_ptr(), dwg.data_ptr(),
+            dwu.data_ptr(), dwd.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev))
+    L.check(rc, "moe_swiglu_bwd_f32" if f32 else "moe_swiglu_bwd")
     return dxp, dwg, dwu, dwd

@@ -29,8 +29,9 @@ expert i's slices as ``w_gate.weight`` etc., and ``state_dict`` /
 ``load_state_dict`` use the reference's per-expert keys
 (``experts.{i}.w_gate.weight``).  Assigning a different ModuleList to
 ``experts`` (the reference's extension point) switches the layer to calling
-those modules per expert between the dispatch and combine kernels.  bf16 uses
-the fused HIP grouped GEMM; other dtypes call the expert modules per expert.
+those modules per expert between the dispatch and combine kernels.  bf16 and
+fp32 (the reference's default dtype) use the fused HIP grouped GEMM (bf16 or
+fp32 MFMA); other dtypes and shapes call the expert modules per expert.
 """
 
 from __future__ import annotations
@@ -259,7 +260,10 @@ class DistributedMoELayer(nn.Module):
 
     def _fused(self) -> bool:
         return (
-            self.w_gate.dtype == torch.bfloat16
+            # the grouped GEMM's shapes: bf16 H % 8 == 0, fp32 H % 4 == 0, both F % 32 == 0
+            self.w_gate.dtype in (torch.bfloat16, torch.float32)
+            and self.w_gate.shape[-1] % (8 if self.w_gate.dtype == torch.bfloat16 else 4) == 0
+            and self.w_gate.shape[1] % 32 == 0
             and all(type(m) is _SwiGLUExpert and m.w_gate._owner() is self for m in self.experts)
             and len(self.experts) == self.num_experts
         )
@@ -359,7 +363,7 @@ class DistributedMoELayer(nn.Module):
         the gate/up and down projections run on the fp8 MFMA with per-row x per-channel scales, the
         SwiGLU activations are quantized per row between them, and the combine is the bf16 one.  Needs
         the fused bf16 expert layout (``self._fused()``) and hidden_dim % 16 == 0."""
-        if not self._fused():
+        if not self._fused() or self.w_gate.dtype != torch.bfloat16:
             raise NotImplementedError("forward_fp8 needs the built-in SwiGLU experts in bfloat16")
         shape = tokens.shape
         flat = tokens.reshape(-1, shape[-1])

@@ -258,6 +258,19 @@ int moe_swiglu_bwd(const void* dy, const void* xp, const void* act, const void* 
                    int64_t F, int64_t E, void* dh, void* dxp, void* dw_gate, void* dw_up, void* dw_down,
                    void* workspace, size_t ws_bytes, void* stream);
 
+/* The same grouped SwiGLU products in float32 (the reference module's default dtype): every tensor fp32,
+ * v_mfma_f32_32x32x2_f32 (fp32 products and sums, as the reference's float32 F.linear experts compute them,
+ * moe_layer.py L:166-198, L:326-337).  Limits: H % 4 == 0, F % 32 == 0, E <= 1024; the operands 16-byte
+ * aligned.  Workspace: moe_swiglu_f32_workspace(E) bytes. */
+size_t moe_swiglu_f32_workspace(int64_t E);
+int moe_swiglu_fwd_f32(const float* xp, const float* w_gate, const float* w_up, const float* w_down,
+                       const int32_t* offsets, int64_t R, int64_t H, int64_t F, int64_t E,
+                       float* act, float* hgu, float* y, void* workspace, size_t ws_bytes, void* stream);
+int moe_swiglu_bwd_f32(const float* dy, const float* xp, const float* act, const float* hgu, const float* w_gate,
+                       const float* w_up, const float* w_down, const int32_t* offsets, int64_t R, int64_t H,
+                       int64_t F, int64_t E, float* dh, float* dxp, float* dw_gate, float* dw_up, float* dw_down,
+                       void* workspace, size_t ws_bytes, void* stream);
+
 /* ----------------------------------------------------------------------
  * fp8 (e4m3, OCP) forward of the expert FFN: a variant of moe_permute +
  * moe_swiglu_fwd (moe_layer.py L:317-319 and the expert loop L:166-198,

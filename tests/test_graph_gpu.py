@@ -64,15 +64,18 @@ def test_router_step_graph_replays_match_eager(shape):
     _replays_match_eager(step, ("idx", "w", "aux", "z", "logits", "cnt", "dx", "dw"))
 
 
-def test_layer_step_graph_replays_match_eager():
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_layer_step_graph_replays_match_eager(dt):
+    """The whole layer step (float32 too: the fp32 grouped GEMM, with no host synchronisation anywhere in the
+    step, which capture would reject) replayed as a graph, bit-identical to the eager step."""
     H, Fd, E, K, N = 256, 512, 8, 2, 512
-    say(f"[graph layer] H{H} F{Fd} E{E} K{K} N{N}")
+    say(f"[graph layer] H{H} F{Fd} E{E} K{K} N{N} {dt}")
     d = dev()
     torch.manual_seed(7)
-    layer = DistributedMoELayer(H, Fd, E, K, build_topology(), dtype=torch.bfloat16, layout="reference",
+    layer = DistributedMoELayer(H, Fd, E, K, build_topology(), dtype=dt, layout="reference",
                                 aux_loss_coef=0.01, z_loss_coef=1e-3, check_numerics=False).to(d)
-    x = torch.randn(N, H, device=d).to(torch.bfloat16).requires_grad_(True)
-    gout = torch.randn(N, H, device=d).to(torch.bfloat16)
+    x = torch.randn(N, H, device=d).to(dt).requires_grad_(True)
+    gout = torch.randn(N, H, device=d).to(dt)
     one = torch.ones((), device=d)
     params = [x, layer.router.gate_w, layer.w_gate, layer.w_up, layer.w_down]
 
