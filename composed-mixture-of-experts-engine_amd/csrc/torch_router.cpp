@@ -41,10 +41,18 @@ int code_of(const at::Tensor& t) { return t.scalar_type() == at::kBFloat16 ? MOE
 
 // The forward's workspace holds a ticket counter that must be zero when a launch starts and that the kernels
 // leave at zero: one zero-initialised buffer per (device, stream), reused by every call on that stream (stream
-// order serialises them).  Under graph capture a fresh zeroed buffer is made instead (a captured fill kernel),
-// so every replay starts from zero.
+// order serialises them).  Under graph capture each capture takes a fresh slice of a per-device arena instead,
+// zeroed and synchronised once outside any capture (on the first eager call): the kernels leave the counter at
+// zero after every replay, so that slice serves every replay of its graph, and the graph holds no fill node.
+// Captures past the arena's end fall back to a zeroed buffer made inside the capture (a captured fill kernel).
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, at::Tensor> g_ws;
+constexpr int64_t kArenaBytes = 32 << 20;
+struct CaptureArena {
+  at::Tensor buf;
+  int64_t used = 0;
+};
+std::map<int, CaptureArena> g_arena;
 
 at::Tensor fwd_workspace(size_t nbytes, const at::Device& dev, hipStream_t s) {
   const int64_t n = std::max<int64_t>((int64_t)nbytes, 1);
@@ -54,8 +62,24 @@ at::Tensor fwd_workspace(size_t nbytes, const at::Device& dev, hipStream_t s) {
     (void)hipGetLastError();
     throw std::runtime_error("moe_router_fwd: hipStreamIsCapturing failed");
   }
-  if (st != hipStreamCaptureStatusNone) return at::zeros({n}, opts);
   std::lock_guard<std::mutex> lk(g_ws_mu);
+  CaptureArena& ar = g_arena[(int)dev.index()];
+  if (st != hipStreamCaptureStatusNone) {
+    const int64_t n256 = (n + 255) / 256 * 256;
+    if (ar.buf.defined() && ar.used + n256 <= kArenaBytes) {
+      at::Tensor slice = ar.buf.narrow(0, ar.used, n);
+      ar.used += n256;
+      return slice;
+    }
+    return at::zeros({n}, opts);
+  }
+  if (!ar.buf.defined()) {
+    ar.buf = at::zeros({kArenaBytes}, opts);
+    if (hipStreamSynchronize(s) != hipSuccess) {  // once: later captures may replay on any stream
+      (void)hipGetLastError();
+      throw std::runtime_error("moe_router_fwd: hipStreamSynchronize failed");
+    }
+  }
   auto& buf = g_ws[{(int)dev.index(), s}];
   if (!buf.defined() || buf.numel() < n) buf = at::zeros({n}, opts);
   return buf;

@@ -214,18 +214,31 @@ def stream_of(device: torch.device) -> int:
 
 
 _ws_cache = {}
+_ARENA_BYTES = 32 << 20
+_capture_arena = {}  # device index -> [zeroed buffer, bytes handed out]
 
 
 def workspace(nbytes: int, device: torch.device, key: Optional[str] = None) -> torch.Tensor:
     """Scratch memory for one call.  With ``key``, a workspace that must start zeroed and that the kernels
     leave zeroed where it matters (the router forward's ticket counter): one zero-initialised buffer per
     (key, device, stream), reused by every call on that stream (stream order serialises them).  Under
-    graph capture a fresh zeroed buffer is made instead, so each replay zeroes it again."""
+    graph capture each capture takes a fresh slice of a per-device arena zeroed (and synchronised) once
+    outside any capture, so the graph holds no fill node (a zeroed buffer made inside the capture once the
+    arena is used up)."""
     n = max(int(nbytes), 1)
     if key is None:
         return torch.empty(n, dtype=torch.uint8, device=device)
+    arena = _capture_arena.get(device.index)
     if torch.cuda.is_current_stream_capturing():
+        n256 = (n + 255) // 256 * 256
+        if arena is not None and arena[1] + n256 <= _ARENA_BYTES:
+            buf = arena[0].narrow(0, arena[1], n)
+            arena[1] += n256
+            return buf
         return torch.zeros(n, dtype=torch.uint8, device=device)
+    if arena is None:
+        _capture_arena[device.index] = [torch.zeros(_ARENA_BYTES, dtype=torch.uint8, device=device), 0]
+        torch.cuda.current_stream(device).synchronize()  # once: later captures may replay on any stream
     stream = torch.cuda.current_stream(device).cuda_stream
     k = (key, device.index, stream)
     buf = _ws_cache.get(k)
