@@ -82,6 +82,10 @@ struct GemmArgs {
   const float* sa;     // mode 2: scale of each A row [rows]
   const float* sb;     // mode 2: scale of each B row [E][N] (EPI1: gate rows [E][F])
   const float* sb2;    // mode 2, EPI1: scale of the up rows [E][F]
+  uint8_t* aq;         // mode 2, EPI1: act block-quantized (e4m3 [rows][F]) ...
+  uint8_t* aqs;        // ... and its E8M0 block scales, slice-major: [(f / 128) * srows + row] * 4 + (f / 32) % 4
+  const uint8_t* mxs;  // mode 2, EPI0: the A operand's E8M0 block scales in that layout (A's rows are act's)
+  int64_t srows;       // rows per slice of the block-scale layout (a multiple of 4)
   int E;
   int M, N, K;         // k-grouped: M, N fixed; row-grouped: N, K fixed
 };
@@ -123,6 +127,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
   __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds) : "memory");
 }
+
 
 // s_waitcnt vmcnt(n) lgkmcnt(0).
 template <int N>
@@ -189,9 +194,21 @@ __device__ __forceinline__ i32x8 frag_rows_f8(const uint8_t* t, int base, int s,
   const u32x4 hi = __builtin_bit_cast(u32x4, frag_rows(t, base, 2 * s + 1, lane));
   return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
-// e4m3 x e4m3 -> fp32 (block scales 127 = 1.0: the per-row / per-column scales are applied in the epilogue)
+// e4m3 x e4m3 -> fp32 (block scales 127 = 1.0: the per-row / per-column scales are applied in the epilogue).
+// With E8M0 block scales the instruction takes k as two blocks of 32 (k 0-31, 32-63 of the step): the first 16
+// bytes of every lane's operand lie in block 0 and the last 16 in block 1 (the layout frag_rows_f8 builds:
+// chunks 4s + h and 4s + 2 + h), lane i (< 32) supplies row i's scale of block 0 and lane i + 32 row i's scale of
+// block 1 (checked on the GPU with one-hot scale patterns).
 __device__ __forceinline__ f32x16 mfma32x32x64_f8(const i32x8& a, const i32x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+// Smallest e with amax <= 448 * 2^e (448 = 0.875 * 2^9), clamped to [-127, 127]; -127 for amax == 0.
+__device__ __forceinline__ int mx_exponent(float amax) {
+  if (!(amax > 0.f)) return -127;
+  int p;
+  const float m = frexpf(amax, &p);
+  const int e = m <= 0.875f ? p - 9 : p - 8;
+  return e < -127 ? -127 : (e > 127 ? 127 : e);
 }
 
 template <int AMODE, int BMODE, int GROUP, int EPI, int NW>
@@ -203,8 +220,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   constexpr int NW_N = GBN / GWN;
   constexpr int MI = GWM / 32, NI = GWN / 32;
   constexpr bool F8 = AMODE == 2;
+  // fp8 down projection: A (act) carries E8M0 block scales, staged per slice beside the ring (2 x 2 KB)
+  constexpr bool MX = F8 && EPI == 0;
+  constexpr int MXSTAGE = 2048;
   static_assert((AMODE == 2) == (BMODE == 2), "fp8 mode applies to both operands");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[GSMEM + (F8 ? GSCALE : 0)];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GSMEM + (F8 ? GSCALE : 0) + (MX ? 2 * MXSTAGE : 0)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -276,43 +296,86 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   // 128-byte line per row); cols mode -> k-rows 2j + l/32, slot l%32.  Rows / columns past the
   // tile are clamped to valid ones (their results are never stored), so a stage that lies wholly
   // inside the reduction range needs only a wave-uniform step per instruction: rows mode adds k0
-  // elements, cols mode k0 * ld. ----
+  // elements, cols mode k0 * ld.  Most kernels keep each source as a 64-bit address (a_src, b_src,
+  // b_src2) and the lane's first k within a stage (a_kl, b_kl); the fp8 down projection (rows mode),
+  // whose block scales leave it no registers to spare, keeps a wave-uniform base and the lane's 32-bit
+  // element offset (a_off, b_off) and recomputes the k. ----
   const uint16_t* a_src[QPW];
   const uint16_t* b_src[QPW];
   const uint16_t* b_src2[QPW];
-  int a_kl[QPW], b_kl[QPW];  // the lane's first k within a stage
+  int a_kl_[QPW], b_kl_[QPW];
+  uint32_t a_off_[QPW], b_off_[QPW];
+  // k slot (l%8) ^ ((i/2)%8) of row i = 8j + l/8, times 8 elements
+  auto kl_rows = [&](int q) { return ((lane & 7) ^ (((8 * (QPW * wv + q) + (lane >> 3)) >> 1) & 7)) * 8; };
+  auto a_kl = [&](int q) {
+    if constexpr (MX) return kl_rows(q);
+    else return a_kl_[q];
+  };
+  auto b_kl = [&](int q) {
+    if constexpr (MX) return kl_rows(q);
+    else return b_kl_[q];
+  };
+  // the bases of the offsets: A rows from mbase, B rows from n0
+  const uint16_t* const a_base = g.A + (int64_t)mbase * g.lda + kbase;
+  const uint16_t* const b_base = g.B + (int64_t)e * g.b_estride + (int64_t)n0 * g.ldb;
+  // In the offsets' uses an empty asm keeps the compiler from hoisting the 64-bit sums out of the k loop
+  // (which would hold two VGPRs per source again).
+  auto a_at = [&](int q, int64_t step) -> const uint16_t* {
+    if constexpr (MX) {
+      uint32_t o = a_off_[q];
+      __asm__("" : "+v"(o));
+      return a_base + step + o;
+    } else {
+      return a_src[q] + step;
+    }
+  };
+  auto b_at = [&](int q, int64_t step) -> const uint16_t* {
+    if constexpr (MX) {
+      uint32_t o = b_off_[q];
+      __asm__("" : "+v"(o));
+      return b_base + step + o;
+    } else {
+      return b_src[q] + step;
+    }
+  };
 #pragma unroll
   for (int q = 0; q < QPW; ++q) {
     const int j = QPW * wv + q;
+    if constexpr (MX) {
+      const int ia = min(8 * j + (lane >> 3), mlen - 1), ib = min(8 * j + (lane >> 3), nlen - 1);
+      a_off_[q] = (uint32_t)(ia * g.lda + kl_rows(q));
+      b_off_[q] = (uint32_t)(ib * g.ldb + kl_rows(q));
+      continue;
+    }
     if constexpr (AMODE != 1) {
       const int i = 8 * j + (lane >> 3);
-      a_kl[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
-      a_src[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase + a_kl[q];
+      a_kl_[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
+      a_src[q] = g.A + (int64_t)(mbase + min(i, mlen - 1)) * g.lda + kbase + a_kl_[q];
     } else {
-      a_kl[q] = 2 * j + (lane >> 5);
-      const int i = (((lane & 31) ^ ((a_kl[q] & 3) << 2)) << 3);
-      a_src[q] = g.A + (int64_t)(kbase + a_kl[q]) * g.lda + mbase + (i < mlen ? i : 0);
+      a_kl_[q] = 2 * j + (lane >> 5);
+      const int i = (((lane & 31) ^ ((a_kl_[q] & 3) << 2)) << 3);
+      a_src[q] = g.A + (int64_t)(kbase + a_kl_[q]) * g.lda + mbase + (i < mlen ? i : 0);
     }
     b_src2[q] = nullptr;
     if constexpr (BMODE != 1) {
       const int i = 8 * j + (lane >> 3);
-      b_kl[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
+      b_kl_[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
       const int ic = min(i, nlen - 1);
       if constexpr (EPI == 1) {
         const int f = nt * (GBN / 2) + (ic >> 6) * 32 + (ic & 31);
-        b_src[q] = (((ic >> 5) & 1) ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)f * g.ldb + b_kl[q];
+        b_src[q] = (((ic >> 5) & 1) ? g.B2 : g.B) + (int64_t)e * g.b_estride + (int64_t)f * g.ldb + b_kl_[q];
       } else {
-        b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)(n0 + ic) * g.ldb + b_kl[q];
+        b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)(n0 + ic) * g.ldb + b_kl_[q];
       }
     } else {
-      b_kl[q] = 2 * j + (lane >> 5);
-      int i = (((lane & 31) ^ ((b_kl[q] & 3) << 2)) << 3);
+      b_kl_[q] = 2 * j + (lane >> 5);
+      int i = (((lane & 31) ^ ((b_kl_[q] & 3) << 2)) << 3);
       i = i < nlen ? i : 0;
       if constexpr (GROUP == 0) {
-        b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)b_kl[q] * g.ldb + n0 + i;
-        if (g.b_split > 0) b_src2[q] = g.B2 + (int64_t)e * g.b_estride + (int64_t)b_kl[q] * g.ldb + n0 + i;
+        b_src[q] = g.B + (int64_t)e * g.b_estride + (int64_t)b_kl_[q] * g.ldb + n0 + i;
+        if (g.b_split > 0) b_src2[q] = g.B2 + (int64_t)e * g.b_estride + (int64_t)b_kl_[q] * g.ldb + n0 + i;
       } else {
-        b_src[q] = g.B + (int64_t)(kbase + b_kl[q]) * g.ldb + n0 + i;
+        b_src[q] = g.B + (int64_t)(kbase + b_kl_[q]) * g.ldb + n0 + i;
       }
     }
   }
@@ -327,11 +390,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     const int64_t step = AMODE != 1 ? (int64_t)k0 : (int64_t)k0 * g.lda;
     if (k0 + GBK <= klen) {
 #pragma unroll
-      for (int q = 0; q < QPW; ++q) lds_dma16(a_src[q] + step, lds_addr(sa + q * 1024));
+      for (int q = 0; q < QPW; ++q) lds_dma16(a_at(q, step), lds_addr(sa + q * 1024));
     } else {
 #pragma unroll
       for (int q = 0; q < QPW; ++q)
-        lds_dma16(k0 + a_kl[q] < klen ? a_src[q] + step : g_zero16, lds_addr(sa + q * 1024));
+        lds_dma16(k0 + a_kl(q) < klen ? a_at(q, step) : g_zero16, lds_addr(sa + q * 1024));
     }
   };
   auto issue_b = [&](int kt, uint8_t* unit) {
@@ -345,11 +408,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       const int64_t step = (int64_t)k0 * bld;
       if (kfull) {
 #pragma unroll
-        for (int q = 0; q < QPW; ++q) lds_dma16(b_src[q] + step, lds_addr(sb + q * 1024));
+        for (int q = 0; q < QPW; ++q) lds_dma16(b_at(q, step), lds_addr(sb + q * 1024));
       } else {
 #pragma unroll
         for (int q = 0; q < QPW; ++q)
-          lds_dma16(k0 + b_kl[q] < klen ? b_src[q] + step : g_zero16, lds_addr(sb + q * 1024));
+          lds_dma16(k0 + b_kl(q) < klen ? b_at(q, step) : g_zero16, lds_addr(sb + q * 1024));
       }
     } else {
       const int64_t step1 = (int64_t)k0 * bld, step2 = (int64_t)(k0 - g.b_split) * bld;
@@ -359,7 +422,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       } else {
 #pragma unroll
         for (int q = 0; q < QPW; ++q) {
-          const int k = k0 + b_kl[q];
+          const int k = k0 + b_kl(q);
           const uint16_t* src = k >= klen ? g_zero16 : (k < g.b_split ? b_src[q] + step1 : b_src2[q] + step2);
           lds_dma16(src, lds_addr(sb + q * 1024));
         }
@@ -405,37 +468,89 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   // are refilled with stage kt+2 while the last quarter's MFMAs run.
   if constexpr (F8) {
     // fp8: two 64-k steps per slice; each step's fragments are read and consumed in turn (the other wave
-    // of the SIMD covers the read latency), one barrier per slice as above
+    // of the SIMD covers the read latency), one barrier per slice as above.  With block-scaled A (MX) each
+    // slice also brings the A rows' E8M0 scales of its four 32-k blocks: a 2 KB window from the 4-row-aligned
+    // row below the tile's first (srows is a multiple of 4, so it is 16-byte aligned), one 256-byte DMA per
+    // wave, and each lane passes its row's scale of the block it supplies to the MFMA.
+    uint8_t* const mx_lds = smem + GSMEM + GSCALE;
+    const int mx_r0 = mbase & 3;
+    auto issue_mx = [&](int kt) {
+      if constexpr (MX) {
+        const uint8_t* src = g.mxs + ((int64_t)kt * g.srows + (mbase - mx_r0)) * 4 + wv * 256 + lane * 16;
+        if (lane < 16) lds_dma16(src, lds_addr(mx_lds + (kt & 1) * MXSTAGE + wv * 256));
+      }
+    };
+    constexpr int MXI = MX ? 1 : 0;  // DMA instructions per wave per slice for the scales
     if (nk > 0) {
       issue_unit(0);
       issue_unit(1);
+      issue_mx(0);
       if (nk > 1) {
         issue_unit(2);
         issue_unit(3);
+        issue_mx(1);
       }
-      if (nk > 1) wait_vmcnt<2 * QPW>();
+      if (nk > 1) wait_vmcnt<2 * QPW + MXI>();
       else wait_vmcnt<0>();
       lds_barrier();
       for (int kt = 0; kt < nk; ++kt) {
         const uint8_t* const ca = unit_ptr(2 * kt);
         const uint8_t* const cb = unit_ptr(2 * kt + 1);
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          i32x8 fa[MI], fb[NI];
-#pragma unroll
-          for (int mi = 0; mi < MI; ++mi) fa[mi] = frag_rows_f8(ca, wm0 + mi * 32, st, lane);
-#pragma unroll
-          for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(cb, wn0 + ni * 32, st, lane);
+        if constexpr (MX) {
+          // the slice's four block scales of each of the lane's MI rows (one 4-byte LDS word per row), shifted
+          // so that byte 2 st of the word is block 2 st + h: lane half h supplies the scale of the step's block h
+          int sw[MI];
 #pragma unroll
           for (int mi = 0; mi < MI; ++mi)
+            sw[mi] = (int)(*reinterpret_cast<const uint32_t*>(
+                         mx_lds + (kt & 1) * MXSTAGE + (mx_r0 + wm0 + mi * 32 + (lane & 31)) * 4) >>
+                     (8 * (lane >> 5)));
+          // the step's B fragments, then A one 32-row block at a time (the next block's read issued before the
+          // current block's MFMAs): two A fragments live instead of MI, which keeps the scales' registers and
+          // the DMA addresses out of scratch
 #pragma unroll
-            for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32x32x64_f8(fa[mi], fb[ni], acc[mi][ni]);
+          for (int st = 0; st < 2; ++st) {
+            i32x8 fb[NI];
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(cb, wn0 + ni * 32, st, lane);
+            i32x8 fa = frag_rows_f8(ca, wm0, st, lane);
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi) {
+              i32x8 fn;
+              if (mi + 1 < MI) fn = frag_rows_f8(ca, wm0 + (mi + 1) * 32, st, lane);
+#pragma unroll
+              for (int ni = 0; ni < NI; ++ni) {
+                if (st == 0)
+                  acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb[ni], acc[mi][ni], 0, 0, 0,
+                                                                                sw[mi], 0, 127);
+                else
+                  acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb[ni], acc[mi][ni], 0, 0, 2,
+                                                                                sw[mi], 0, 127);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+              if (mi + 1 < MI) fa = fn;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int st = 0; st < 2; ++st) {
+            i32x8 fa[MI], fb[NI];
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi) fa[mi] = frag_rows_f8(ca, wm0 + mi * 32, st, lane);
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(cb, wn0 + ni * 32, st, lane);
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+              for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32x32x64_f8(fa[mi], fb[ni], acc[mi][ni]);
+          }
         }
         wait_vmcnt_lgkm0<0>();  // stage kt+1 landed; this wave's reads of stage kt are done
         lds_barrier();
         if (kt + 2 < nk) {
           issue_unit(2 * kt + 4);
           issue_unit(2 * kt + 5);
+          issue_mx(kt + 2);
         }
       }
       wait_vmcnt<0>();
@@ -459,8 +574,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       if (p < QPW) {
         const int q = p;
         const int64_t step = AMODE != 1 ? (int64_t)k0 : (int64_t)k0 * g.lda;
-        if (full) return a_src[q] + step;
-        return (k0 + a_kl[q] < klen) ? a_src[q] + step : g_zero16;
+        if (full) return a_at(q, step);
+        return (k0 + a_kl(q) < klen) ? a_at(q, step) : g_zero16;
       }
       const int q = p - QPW;
       const int64_t bld = BMODE != 1 ? 1 : g.ldb;
@@ -468,14 +583,14 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         if constexpr (BMODE == 1 && GROUP == 0) {
           if (g.b_split > 0 && k0 >= g.b_split) return b_src2[q] + (int64_t)(k0 - g.b_split) * bld;
         }
-        return b_src[q] + (int64_t)k0 * bld;
+        return b_at(q, (int64_t)k0 * bld);
       }
-      const int k = k0 + b_kl[q];
+      const int k = k0 + b_kl(q);
       if (k >= klen) return g_zero16;
       if constexpr (BMODE == 1 && GROUP == 0) {
         if (g.b_split > 0 && k >= g.b_split) return b_src2[q] + (int64_t)(k0 - g.b_split) * bld;
       }
-      return b_src[q] + (int64_t)k0 * bld;
+      return b_at(q, (int64_t)k0 * bld);
     };
     auto slice_full = [&](int kt) {
       const int k0 = kt * GBK;
@@ -615,7 +730,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     // the tile's row scales [256] and column scales [256] (rows / columns past the tile clamped)
     float* s_sc = reinterpret_cast<float*>(smem + GSMEM);
     if (tid < 256) {
-      s_sc[tid] = g.sa[mbase + min(tid, mlen - 1)];
+      s_sc[tid] = MX ? 1.f : g.sa[mbase + min(tid, mlen - 1)];  // MX: the row scales were applied per block
       float sb;
       if constexpr (EPI == 1) {
         const int f = min(nt * (GBN / 2) + (tid >> 6) * 32 + (tid & 31), g.F - 1);
@@ -654,6 +769,57 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   if constexpr (EPI == 1) {
     // tile column c: pair c/64, gate (c/32 even) or up (odd), f = nt*BN/2 + (c/64)*32 + c%32
     constexpr int UPR = BN / 16;  // gate chunks of 8 per row
+    static_assert((BM * UPR) % NT == 0 && NT % 16 == 0, "every thread runs the same chunks of whole rows");
+    if constexpr (F8) {
+      if (g.aq != nullptr) {
+        // act block-quantized for the down projection (the tile's 128 f are that product's k slice nt): the
+        // four consecutive threads of one 32-f block (same row; q % 4 = 0..3) share its absmax, the block's
+        // E8M0 exponent e is the smallest with absmax <= 448 * 2^e, and each element x * 2^-e (exact) is
+        // rounded to e4m3; blocks past F get the scale byte of 1.0
+        for (int u = tid; u < BM * UPR; u += NT) {
+          const int r = u / UPR, q = u % UPR;
+          const int cc = (q >> 2) * 64 + (q & 3) * 8;
+          const int f = nt * (BN / 2) + (q >> 2) * 32 + (q & 3) * 8;
+          const bool ok = r < mlen && f < g.F;
+          const u32x4 gv = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc]);
+          const u32x4 uv = *reinterpret_cast<const u32x4*>(&cs[r * CP + cc + 32]);
+          u32x4 av;
+          float a[8];
+          float amax = 0.f;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const float g0 = __uint_as_float(gv[d] << 16), g1 = __uint_as_float(gv[d] & 0xffff0000u);
+            const float u0 = __uint_as_float(uv[d] << 16), u1 = __uint_as_float(uv[d] & 0xffff0000u);
+            av[d] = pack2bf(silu_f(g0) * u0, silu_f(g1) * u1);
+            a[2 * d] = __uint_as_float(av[d] << 16);
+            a[2 * d + 1] = __uint_as_float(av[d] & 0xffff0000u);
+            amax = fmaxf(amax, fmaxf(fabsf(a[2 * d]), fabsf(a[2 * d + 1])));
+          }
+          amax = ok ? amax : 0.f;
+          amax = fmaxf(amax, __shfl_xor(amax, 1));
+          amax = fmaxf(amax, __shfl_xor(amax, 2));
+          const int ex = mx_exponent(amax);
+          const float sc = ldexpf(1.f, -ex);
+          const int64_t row = mbase + r;
+          if (ok) {
+            int lo = 0, hi = 0;
+            lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[0] * sc, a[1] * sc, lo, false);
+            lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[2] * sc, a[3] * sc, lo, true);
+            hi = __builtin_amdgcn_cvt_pk_fp8_f32(a[4] * sc, a[5] * sc, hi, false);
+            hi = __builtin_amdgcn_cvt_pk_fp8_f32(a[6] * sc, a[7] * sc, hi, true);
+            *reinterpret_cast<uint2*>(g.aq + row * g.F + f) = uint2{(unsigned)lo, (unsigned)hi};
+            if (g.C != nullptr) *reinterpret_cast<u32x4*>(g.C + row * g.ldc + f) = av;
+            if (g.C2 != nullptr) {
+              *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + f) = gv;
+              *reinterpret_cast<u32x4*>(g.C2 + row * 2 * (int64_t)g.F + g.F + f) = uv;
+            }
+          }
+          if (r < mlen && (q & 3) == 0)
+            g.aqs[((int64_t)nt * g.srows + row) * 4 + (q >> 2)] = (uint8_t)(f < g.F ? ex + 127 : 127);
+        }
+        return;
+      }
+    }
     for (int u = tid; u < BM * UPR; u += NT) {
       const int r = u / UPR, q = u % UPR;
       const int cc = (q >> 2) * 64 + (q & 3) * 8;  // gate column of this chunk
@@ -866,9 +1032,21 @@ extern "C" int moe_swiglu_fwd(const void* xp, const void* w_gate, const void* w_
   return launch<0, 0, 0, 0, kNW_fwd2>("k_gemm_swiglu_fwd2", s, b, R);
 }
 
+namespace moe {
+namespace {
+// fp8 forward workspace: tile prefix + expert order, then act in e4m3 [R, F], then its E8M0 block scales in the
+// slice-major layout [(F / 128 slices) x srows rows x 4 blocks] (srows = R rounded up to 4) plus one 2 KB
+// window of slack (the down projection stages 2 KB per slice from a tile's 4-aligned first row).
+size_t fp8_act_bytes(int64_t R, int64_t F) { return ((size_t)R * F + 255) & ~(size_t)255; }
+int64_t fp8_srows(int64_t R) { return (R + 3) / 4 * 4; }
+size_t fp8_scale_bytes(int64_t R, int64_t F) {
+  return (((size_t)((F + 127) / 128) * fp8_srows(R) * 4 + 2048) + 255) & ~(size_t)255;
+}
+}  // namespace
+}  // namespace moe
+
 extern "C" size_t moe_swiglu_fwd_fp8_workspace(int64_t R, int64_t F, int64_t E) {
-  // tile prefix + expert order, then act in e4m3 [R, F] and its row scales [R]
-  return moe_swiglu_workspace(E) + (((size_t)R * F + 255) & ~(size_t)255) + (((size_t)R * 4 + 255) & ~(size_t)255);
+  return moe_swiglu_workspace(E) + fp8_act_bytes(R, F) + fp8_scale_bytes(R, F);
 }
 
 extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* wg_q, const float* sg, const void* wu_q,
@@ -879,8 +1057,8 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
     return fail_arg("moe_swiglu_fwd_fp8: bad shape R=%lld H=%lld F=%lld E=%lld (need H%%16==0, F%%32==0)",
                     (long long)R, (long long)H, (long long)F, (long long)E);
   if (R == 0) return 0;
-  if (!xq || !sx || !wg_q || !sg || !wu_q || !su || !wd_q || !sd || !offsets || !act || !y || !a16(xq) ||
-      !a16(wg_q) || !a16(wu_q) || !a16(wd_q) || !a16(act) || (hgu && !a16(hgu)) || !a16(y))
+  if (!xq || !sx || !wg_q || !sg || !wu_q || !su || !wd_q || !sd || !offsets || !y || !a16(xq) || !a16(wg_q) ||
+      !a16(wu_q) || !a16(wd_q) || (act && !a16(act)) || (hgu && !a16(hgu)) || !a16(y))
     return fail_arg("moe_swiglu_fwd_fp8: null or misaligned pointer");
   if (ws_bytes < moe_swiglu_fwd_fp8_workspace(R, F, E) || !workspace)
     return set_error("moe_swiglu_fwd_fp8: workspace"), MOE_EWORKSPACE;
@@ -889,7 +1067,7 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
   int* tile_off = reinterpret_cast<int*>(ws);
   int* korder = tile_off + (E + 1);
   uint8_t* actq = reinterpret_cast<uint8_t*>(ws + moe_swiglu_workspace(E));
-  float* sact = reinterpret_cast<float*>(ws + moe_swiglu_workspace(E) + (((size_t)R * F + 255) & ~(size_t)255));
+  uint8_t* sact = reinterpret_cast<uint8_t*>(ws + moe_swiglu_workspace(E) + fp8_act_bytes(R, F));
   MOE_LAUNCH("k_gemm_tiles", k_gemm_tiles, dim3(1), dim3(1024), 0, s, offsets, (int)E, kTileBM, tile_off, korder);
   // fwd1: [act | hgu] = (xq sx) . ([Wg ; Wu] [sg ; su])^T; fp8 matrices are addressed in 16-bit units
   GemmArgs a{};
@@ -906,15 +1084,16 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
   a.sa = sx;
   a.sb = sg;
   a.sb2 = su;
-  a.C = static_cast<uint16_t*>(act);
+  a.C = static_cast<uint16_t*>(act);  // optional: act in bf16 as well
   a.C2 = static_cast<uint16_t*>(hgu);
   a.ldc = F;
   a.N = (int)(2 * F);
   a.K = (int)(H / 2);
+  a.aq = actq;  // act block-quantized in the epilogue (e4m3 + E8M0 scale per 32 f)
+  a.aqs = sact;
+  a.srows = fp8_srows(R);
   if (int rc = launch<2, 2, 0, 1, kNW_fp8>("k_gemm_swiglu_fwd1_fp8", s, a, R)) return rc;
-  // act -> e4m3 with a scale per row, then fwd2: y = (actq sact) . (Wd sd)^T
-  // (rows past offsets[E] are never read by the down projection and are not quantized)
-  if (int rc = quant_rows_fp8(act, MOE_BF16, R, F, F, actq, sact, offsets + E, s)) return rc;
+  // fwd2: y = (actq 2^e per block) . (Wd sd)^T, the block scales applied inside the MFMA
   GemmArgs b{};
   b.offsets = offsets;
   b.tile_off = tile_off;
@@ -925,7 +1104,8 @@ extern "C" int moe_swiglu_fwd_fp8(const void* xq, const float* sx, const void* w
   b.B = static_cast<const uint16_t*>(wd_q);
   b.ldb = F / 2;
   b.b_estride = H * F / 2;
-  b.sa = sact;
+  b.mxs = sact;
+  b.srows = fp8_srows(R);
   b.sb = sd;
   b.C = static_cast<uint16_t*>(y);
   b.ldc = H;

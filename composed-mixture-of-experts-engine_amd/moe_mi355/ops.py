@@ -503,10 +503,13 @@ def permute_fp8(x: torch.Tensor, p: Plan) -> Tuple[torch.Tensor, torch.Tensor]:
     return xq, sx
 
 
-def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, keep_preact: bool = True):
+def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, keep_preact: bool = True,
+                       return_mx: bool = False):
     """fp8 forward of the SwiGLU experts: ``xq`` [R,H] uint8 e4m3 with row scales ``sx`` [R]; ``wq`` =
     (gate [E,F,H], up [E,F,H], down [E,H,F]) e4m3 bytes with ``wscale`` = (sg [E,F], su [E,F], sd [E,H])
-    -> (act [R,F], hgu [R,2F], y [R,H]) bf16, as :func:`swiglu_forward` (hgu None with keep_preact=False)."""
+    -> (act [R,F], hgu [R,2F], y [R,H]) bf16, as :func:`swiglu_forward`; with keep_preact=False (inference)
+    act and hgu are None (the down projection reads act block-quantized from the gate/up epilogue).
+    ``return_mx``: also return (act e4m3 bytes [R, F], E8M0 block scales [R, F/32]) as the kernels wrote them."""
     wg, wu, wd = wq
     sg, su, sd = wscale
     dev = L.require_device(xq, sx, wg, wu, wd, sg, su, sd, offsets)
@@ -517,7 +520,7 @@ def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, ke
         raise TypeError("swiglu_forward_fp8: outputs are bfloat16")
     R, H = xq.shape
     E, F, _ = wg.shape
-    act = torch.empty((R, F), dtype=out_dtype, device=dev)
+    act = torch.empty((R, F), dtype=out_dtype, device=dev) if keep_preact else None
     hgu = torch.empty((R, 2 * F), dtype=out_dtype, device=dev) if keep_preact else None
     y = torch.empty((R, H), dtype=out_dtype, device=dev)
     lib = L.load()
@@ -526,10 +529,20 @@ def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, ke
     rc = lib.moe_swiglu_fwd_fp8(
         xq.data_ptr(), sx.contiguous().data_ptr(), wg.data_ptr(), sg.contiguous().data_ptr(), wu.data_ptr(),
         su.contiguous().data_ptr(), wd.data_ptr(), sd.contiguous().data_ptr(), offsets.data_ptr(), R, H, F, E,
-        act.data_ptr(), L.ptr(hgu), y.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
+        L.ptr(act), L.ptr(hgu), y.data_ptr(), ws.data_ptr(), nbytes, L.stream_of(dev),
     )
     L.check(rc, "moe_swiglu_fwd_fp8")
-    return act, hgu, y
+    if not return_mx:
+        return act, hgu, y
+    # the workspace: tile tables (moe_swiglu_workspace(E) bytes), act in e4m3 [R, F] (256-byte aligned), then
+    # the block scales [F/128 slices][R rounded up to 4][4 blocks]
+    off_a = lib.moe_swiglu_workspace(E)
+    off_s = off_a + (R * F + 255) // 256 * 256
+    srows = (R + 3) // 4 * 4
+    nsl = (F + 127) // 128
+    aq = ws[off_a:off_a + R * F].view(R, F)
+    sc = ws[off_s:off_s + nsl * srows * 4].view(nsl, srows, 4)[:, :R].permute(1, 0, 2).reshape(R, nsl * 4)
+    return act, hgu, y, (aq, sc[:, : F // 32])
 
 
 def swiglu_backward(dy, xp, act, hgu, w_gate, w_up, w_down, offsets):

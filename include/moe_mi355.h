@@ -287,8 +287,14 @@ int moe_swiglu_bwd_f32(const float* dy, const float* xp, const float* act, const
  * empty, or past offsets[E], are not written).
  * moe_swiglu_fwd_fp8: act, hgu, y as moe_swiglu_fwd (bf16) from xq / sx and
  * the quantized weights wg_q, wu_q [E, F, H], wd_q [E, H, F] with scales
- * sg, su [E, F], sd [E, H] (moe_quant_rows_fp8 over the weight rows); act
- * is quantized per row in the workspace before the down projection.
+ * sg, su [E, F], sd [E, H] (moe_quant_rows_fp8 over the weight rows).  The
+ * gate/up epilogue writes act block-quantized into the workspace for the
+ * down projection (OCP MX: every 32 consecutive elements of a row share a
+ * power-of-two scale 2^e, e the smallest integer with absmax <= 448 * 2^e,
+ * stored as the E8M0 byte e + 127; elements x * 2^-e rounded to nearest
+ * even).  Workspace layout after the moe_swiglu_workspace(E) tile tables:
+ * act e4m3 [R, F], then at the next 256-byte boundary the scale bytes
+ * [F / 128][R rounded up to 4][4].  act and hgu may be NULL (inference).
  * H % 16 == 0, F % 32 == 0.
  * ---------------------------------------------------------------------- */
 int moe_quant_rows_fp8(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld, void* dst,

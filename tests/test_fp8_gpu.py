@@ -92,12 +92,18 @@ def test_swiglu_forward_fp8_parity(R, H, F, E, counts):
     d = dev()
     xq, sx = ops.quant_rows_fp8(xp.to(d))
     wq = [ops.quant_rows_fp8(w.to(d)) for w in wts]
-    act, hgu, y = ops.swiglu_forward_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets.to(d))
+    act, hgu, y, (aq, asc) = ops.swiglu_forward_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets.to(d),
+                                                    return_mx=True)
     torch.cuda.synchronize()
     used = int(offsets[-1])
     oq = [O8.quant_rows(w) for w in wts]
     for (q, s), (rq, rs) in zip(wq, oq):
         assert torch.equal(q.cpu(), rq) and torch.equal(s.cpu(), rs)
+    # act block-quantized in the gate/up epilogue: bytes and E8M0 scales bit-exact with the oracle's quant_mx of
+    # the kernel's own act
+    mq, ms = O8.quant_mx(act[:used].cpu().float())
+    assert torch.equal(asc[:used].cpu(), ms), "E8M0 block scales"
+    assert torch.equal(aq[:used].cpu(), mq), "e4m3 bytes of act"
     rh, ra, ry = O8.swiglu_fwd_fp8(xq.cpu(), sx.cpu(), [q for q, _ in oq], [s for _, s in oq], offsets.tolist(),
                                    act_in=act.cpu().float())
     tol = TOL[torch.bfloat16]
@@ -157,7 +163,11 @@ def test_forward_without_preactivations(fp8):
     a1, h1, y1 = run(True)
     a2, h2, y2 = run(False)
     assert h1 is not None and h2 is None
-    assert torch.equal(a1, a2) and torch.equal(y1, y2)
+    assert torch.equal(y1, y2)
+    if fp8:
+        assert a2 is None  # inference: the down projection reads act block-quantized, no bf16 copy
+    else:
+        assert torch.equal(a1, a2)
 
 
 def test_layer_no_grad_matches_training_forward():

@@ -97,3 +97,60 @@ def test_tiny_rows_quantize_to_zeros_not_nan():
     assert bool(torch.isinf(inv).all())
     bad = (v * inv.unsqueeze(-1)).to(torch.float8_e4m3fn).float()
     assert bool(torch.isnan(bad).any())
+
+
+def test_mx_exponent_is_the_smallest_that_fits():
+    """mx_exponent(amax) = min{e integer : amax <= 448 * 2^e} by brute force over e, for random magnitudes,
+    exact powers of two and the 448 * 2^k boundaries (and just past them)."""
+    g = torch.Generator().manual_seed(5)
+    a = torch.cat([torch.rand(2000, generator=g) * torch.logspace(-30, 30, 2000),
+                   torch.pow(2.0, torch.arange(-40.0, 40.0)),
+                   448.0 * torch.pow(2.0, torch.arange(-20.0, 20.0)),
+                   torch.nextafter(448.0 * torch.pow(2.0, torch.arange(-20.0, 20.0)), torch.tensor(1e30))])
+    e = O8.mx_exponent(a)
+    for v, ev in zip(a.double().tolist(), e.tolist()):
+        want = next(k for k in range(-127, 128) if v <= 448.0 * 2.0 ** k)
+        assert ev == want, (v, ev, want)
+
+
+def test_quant_mx_closed_forms():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(40, 256, generator=g) * torch.logspace(-6, 6, 40).unsqueeze(1)
+    x[3, 32:64] = 0.0            # a zero block
+    x[4, :32] = 1.0              # a block of ones: e = -8 (448 * 2^-9 < 1 <= 448 * 2^-8), bytes 2^8 -> 0x78
+    x[4, 32:64] = 448.0          # e = 0, bytes 0x7e, scale byte 127
+    q, sb = O8.quant_mx(x)
+    assert q.shape == x.shape and sb.shape == (40, 8)
+    assert int(sb[3, 1]) == 0 and int(q[3, 32:64].sum()) == 0
+    assert int(sb[4, 0]) == 127 - 8 and set(q[4, :32].tolist()) == {0x78}
+    assert int(sb[4, 1]) == 127 and set(q[4, 32:64].tolist()) == {0x7E}
+    d = O8.dequant_mx(q, sb)
+    blocks = x.double().reshape(40, 8, 32)
+    db = d.reshape(40, 8, 32)
+    for r in range(40):
+        for b in range(8):
+            amax = blocks[r, b].abs().max().item()
+            if amax == 0.0:
+                continue
+            # the scaled block maximum lies in (224, 448]: 448 * 2^e covers it and 448 * 2^(e-1) does not
+            scaled = amax * 2.0 ** -(int(sb[r, b]) - 127)
+            assert 224.0 < scaled <= 448.0, (r, b, scaled)
+            i = int(blocks[r, b].abs().argmax())
+            v = abs(float(q[r, 32 * b + i].view(torch.float8_e4m3fn).float()))
+            assert 224.0 <= v <= 448.0
+    # per element: within the e4m3 rounding bound (relative 2^-4, absolute 2^(e-9) in the subnormal range)
+    scale = torch.pow(2.0, sb.double() - 127.0).repeat_interleave(32, dim=1)
+    bound = torch.maximum(x.double().abs() * 2.0 ** -4, scale * 2.0 ** -9)
+    assert bool(((d - x.double()).abs() <= bound + 1e-300).all())
+
+
+def test_quant_mx_planted_mistake_is_caught():
+    """A plausible off-by-one (e = p - 8 for every block, as a floor(log2) - 8 rule gives) leaves blocks whose
+    scaled maximum is <= 224, which the (224, 448] pin rejects; the oracle's exponent passes it."""
+    x = torch.randn(8, 64, generator=torch.Generator().manual_seed(7))
+    amax = x.reshape(8, 2, 32).abs().amax(-1).double()
+    _m, p = torch.frexp(amax)
+    wrong = (p - 8).double()
+    right = O8.quant_mx(x)[1].double() - 127.0
+    ok = lambda e: bool((((amax * torch.pow(2.0, -e)) > 224.0) & ((amax * torch.pow(2.0, -e)) <= 448.0)).all())
+    assert ok(right) and not ok(wrong)
