@@ -466,7 +466,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   // quarter of stage kt every wave waits for stage kt+1 (the only DMA group in flight) and for its
   // own reads of stage kt; one barrier makes both visible workgroup-wide, and stage kt's two units
   // are refilled with stage kt+2 while the last quarter's MFMAs run.
-  if constexpr (F8) {
+  if constexpr (F8 && NW == 8) {
     // fp8: two 64-k steps per slice; each step's fragments are read and consumed in turn (the other wave
     // of the SIMD covers the read latency), one barrier per slice as above.  With block-scaled A (MX) each
     // slice also brings the A rows' E8M0 scales of its four 32-k blocks: a 2 KB window from the 4-row-aligned
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       wait_vmcnt<0>();
     }
   } else if constexpr (NW == 4) {
-    static_assert(AMODE == 0 && BMODE == 0, "the 4-wave main loop takes k-contiguous operands");
+    static_assert(AMODE == BMODE && AMODE != 1, "the 4-wave main loop takes k-contiguous operands");
     // One wave per SIMD, 128x128 per wave.  The refill goes through registers two slices ahead: while slice
     // kt is computed, each wave writes its share of slice kt+1 (loaded during slice kt-1) into the free LDS
     // slot and loads its share of slice kt+2 into the same registers, one piece (16 bytes a lane) at a time
@@ -610,6 +610,143 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       *reinterpret_cast<u32x4*>(unit_ptr(2 * kt + op) + (QPW * wv + q) * 1024 + lane * 16) = st[p];
       __asm__ volatile("" ::: "memory");
     };
+    if constexpr (F8) {
+      // fp8: each 128-byte k slice is two 64-k steps of MI x NI MFMAs (32x32x64, e4m3).  One fragment set is
+      // live: an A fragment is re-read for the next step right after its row's last MFMA of this step, a B
+      // fragment after its column's (the last row of MFMAs), so the reads of step s+1 run under the MFMAs of
+      // step s without a second set of registers.  The refill pieces of slice kt+1 (LDS writes) and kt+2
+      // (global loads) go one per MFMA slot into step 0 and the first half of step 1; then each wave waits
+      // for its own LDS traffic, one barrier makes slice kt+1 visible, and the second half of step 1 reads
+      // slice kt+1's step-0 fragments as they free up.  With block-scaled A (MX) the slice's scale window (2 KB
+      // from the 4-row-aligned row below the tile's first, as the 8-wave loop stages it) rides along as one
+      // more piece (512 bytes a wave, lanes 32-63 repeating lanes 0-31) into a 2-slot LDS area, and each lane reads its rows' scale
+      // words of slice kt+1 right after that barrier.
+      constexpr int NPX = NP + (MX ? 1 : 0);  // pieces per slice, the scale window last
+      constexpr int PA = NPX - 8;             // pieces in step 0; the other 8 in step 1's first half
+      static_assert(MI * NI == 16 && NI == 4 && PA <= 16, "fp8 4-wave slot plan");
+      uint8_t* const mx_lds = smem + GSMEM + GSCALE;
+      const int mx_r0 = mbase & 3;
+      u32x4 st_mx;
+      auto gload_x = [&](int kt, int p, bool full) {
+        if constexpr (MX) {
+          if (p == NP) {  // lanes 32-63 repeat lanes 0-31 (no divergent branch in the slot sequence)
+            st_mx = *reinterpret_cast<g_u32x4*>(reinterpret_cast<uintptr_t>(
+                g.mxs + ((int64_t)kt * g.srows + (mbase - mx_r0)) * 4 + (wv * 32 + (lane & 31)) * 16));
+            return;
+          }
+        }
+        gload(kt, p, full);
+      };
+      auto lwrite_x = [&](int kt, int p) {
+        if constexpr (MX) {
+          if (p == NP) {
+            __asm__ volatile("" ::: "memory");
+            *reinterpret_cast<u32x4*>(mx_lds + (kt & 1) * MXSTAGE + (wv * 32 + (lane & 31)) * 16) = st_mx;
+            __asm__ volatile("" ::: "memory");
+            return;
+          }
+        }
+        lwrite(kt, p);
+      };
+      i32x8 fa[MI], fb[NI];
+      int sw[MI];
+      uint32_t swn[MI];
+      // the lane's scale word of each of its MI rows for slice kt (raw), and the form the MFMA takes: shifted
+      // so that byte 2 st of the word is block 2 st + h (lane half h supplies the scale of the step's block h);
+      // the shift waits for the read, so it is applied only where the words are taken into use
+      auto read_sw = [&](int kt, uint32_t (&w)[MI]) {
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+          w[mi] = *reinterpret_cast<const uint32_t*>(mx_lds + (kt & 1) * MXSTAGE +
+                                                     (mx_r0 + wm0 + mi * 32 + (lane & 31)) * 4);
+      };
+      auto use_sw = [&](const uint32_t (&w)[MI]) {
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) sw[mi] = (int)(w[mi] >> (8 * (lane >> 5)));
+      };
+      // MFMA slots [SLO, SHI) of step ST (slot i = row i / NI, column i % NI); after slot i the next step's
+      // fragments that it frees are read from (nas, nbs, step nst) when read_next, and refill piece
+      // PLO + (i - SLO) moves when below PHI.  MODE as in the bf16 loop (0: write kt+1 / load full kt+2,
+      // 1: load with checks, 2: write only, 3: none).
+      auto slots = [&](auto st_c, auto slo_c, auto shi_c, auto mode_c, auto plo_c, auto phi_c, const uint8_t* nas,
+                       const uint8_t* nbs, int nst, bool read_next, int kt, bool lfull) {
+        constexpr int ST = decltype(st_c)::value, SLO = decltype(slo_c)::value, SHI = decltype(shi_c)::value;
+        constexpr int MODE = decltype(mode_c)::value, PLO = decltype(plo_c)::value, PHI = decltype(phi_c)::value;
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+          (([&] {
+             constexpr int i = SLO + I;
+             constexpr int mi = i / NI, ni = i % NI;
+             if constexpr (MX)
+               acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[mi], fb[ni], acc[mi][ni], 0, 0,
+                                                                             2 * ST, sw[mi], 0, 127);
+             else
+               acc[mi][ni] = mfma32x32x64_f8(fa[mi], fb[ni], acc[mi][ni]);
+             __builtin_amdgcn_sched_barrier(0);
+             if (read_next) {
+               if constexpr (ni == NI - 1) fa[mi] = frag_rows_f8(nas, wm0 + mi * 32, nst, lane);
+               if constexpr (mi == MI - 1) fb[ni] = frag_rows_f8(nbs, wn0 + ni * 32, nst, lane);
+             }
+             constexpr int p = PLO + I;
+             if constexpr (MODE < 3 && p < PHI) {
+               lwrite_x(kt + 1, p);
+               if constexpr (MODE == 0) gload_x(kt + 2, p, true);
+               else if constexpr (MODE == 1) gload_x(kt + 2, p, lfull);
+             }
+             __builtin_amdgcn_sched_barrier(0);
+           }()), ...);
+        }(std::make_integer_sequence<int, SHI - SLO>{});
+      };
+      using C0 = std::integral_constant<int, 0>;
+      using C1 = std::integral_constant<int, 1>;
+      using C8 = std::integral_constant<int, 8>;
+      using C16 = std::integral_constant<int, 16>;
+      using CPA = std::integral_constant<int, PA>;
+      using CNP = std::integral_constant<int, NPX>;
+      using M3 = std::integral_constant<int, 3>;
+      auto slice = [&](auto mode_c, int kt) {
+        const uint8_t* const ca = unit_ptr(2 * kt);
+        const uint8_t* const cb = unit_ptr(2 * kt + 1);
+        const bool lfull = kt + 2 < nk ? slice_full(kt + 2) : true;
+        slots(C0{}, C0{}, C16{}, mode_c, C0{}, CPA{}, ca, cb, 1, true, kt, lfull);
+        slots(C1{}, C0{}, C8{}, mode_c, CPA{}, CNP{}, ca, cb, 0, false, kt, lfull);
+        wait_vmcnt_lgkm0<63>();  // this wave's LDS writes of slice kt+1 and reads of slice kt are done
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const bool more = kt + 1 < nk;
+        const uint8_t* const na = unit_ptr(2 * kt + 2);
+        const uint8_t* const nb = unit_ptr(2 * kt + 3);
+        if (more) {
+          // rows 0 and 1 finished their MFMAs in the first half of step 1
+#pragma unroll
+          for (int mi = 0; mi < 8 / NI; ++mi) fa[mi] = frag_rows_f8(na, wm0 + mi * 32, 0, lane);
+          if constexpr (MX) read_sw(kt + 1, swn);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        slots(C1{}, C8{}, C16{}, M3{}, C0{}, C0{}, na, nb, 0, more, kt, true);
+        if constexpr (MX) use_sw(swn);
+      };
+      if (nk > 0) {
+        for (int p = 0; p < NPX; ++p) gload_x(0, p, slice_full(0));
+        for (int p = 0; p < NPX; ++p) lwrite_x(0, p);
+        if (nk > 1) {
+          for (int p = 0; p < NPX; ++p) gload_x(1, p, slice_full(1));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) fa[mi] = frag_rows_f8(unit_ptr(0), wm0 + mi * 32, 0, lane);
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(unit_ptr(1), wn0 + ni * 32, 0, lane);
+        if constexpr (MX) {
+          read_sw(0, swn);
+          use_sw(swn);
+        }
+        int kt = 0;
+        for (; kt + 3 < nk && slice_full(kt + 2); ++kt) slice(C0{}, kt);
+        for (; kt + 2 < nk; ++kt) slice(C1{}, kt);
+        if (kt + 1 < nk) slice(std::integral_constant<int, 2>{}, kt++);
+        if (kt < nk) slice(M3{}, kt);
+      }
+    } else {
     auto read_frag = [&](const uint8_t* as, const uint8_t* bs, int ks, int f, i16x8 (&fa)[MI], i16x8 (&fb)[NI]) {
       if (f < MI) fa[f] = frag_rows(as, wm0 + f * 32, ks, lane);
       else fb[f - MI] = frag_rows(bs, wn0 + (f - MI) * 32, ks, lane);
@@ -677,6 +814,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       if (kt + 1 < nk) slice(std::integral_constant<int, 2>{}, kt++);
       if (kt < nk) slice(std::integral_constant<int, 3>{}, kt);
     }
+    }
     wait_vmcnt<0>();
   } else if (nk > 0) {
     issue_unit(0);
@@ -741,6 +879,66 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       s_sc[256 + tid] = sb;
     }
     __syncthreads();
+    if constexpr (EPI == 1) {
+      if (g.aq != nullptr && g.C2 == nullptr) {
+        // inference: no pre-activations to store, so the SwiGLU runs on the accumulators (a lane holds the gate
+        // and the up value of one f in acc[mi][2p][j] and acc[mi][2p + 1][j]: tile columns 64 (c / 64) + c % 32
+        // and + 32) with the same roundings as below (gate and up to bf16, act to bf16), and only act goes
+        // through LDS, as a [256][128 + 8] bf16 tile, for the block quantization (the same per-chunk code as
+        // the general path, reading one 16-byte act chunk instead of the gate and up chunks)
+        constexpr int AP = GBN / 2 + 8;
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int pr = 0; pr < NI / 2; ++pr) {
+            const int cg = wn0 + 2 * pr * 32 + (lane & 31);
+            const float sg = s_sc[256 + cg], su = s_sc[256 + cg + 32];
+            const int fc = (cg >> 6) * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+              const float sr = s_sc[r];
+              const float gq = __uint_as_float((uint32_t)f2bf(acc[mi][2 * pr][j] * sr * sg) << 16);
+              const float uq = __uint_as_float((uint32_t)f2bf(acc[mi][2 * pr + 1][j] * sr * su) << 16);
+              cs[r * AP + fc] = f2bf(silu_f(gq) * uq);
+            }
+          }
+        __syncthreads();
+        constexpr int QPR = GBN / 16;  // 8-f chunks per row
+        for (int u = tid; u < GBM * QPR; u += GNT) {
+          const int r = u / QPR, q = u % QPR;
+          const int f = nt * (GBN / 2) + q * 8;
+          const bool ok = r < mlen && f < g.F;
+          const u32x4 av = *reinterpret_cast<const u32x4*>(&cs[r * AP + q * 8]);
+          float a[8];
+          float amax = 0.f;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            a[2 * d] = __uint_as_float(av[d] << 16);
+            a[2 * d + 1] = __uint_as_float(av[d] & 0xffff0000u);
+            amax = fmaxf(amax, fmaxf(fabsf(a[2 * d]), fabsf(a[2 * d + 1])));
+          }
+          amax = ok ? amax : 0.f;
+          amax = fmaxf(amax, __shfl_xor(amax, 1));
+          amax = fmaxf(amax, __shfl_xor(amax, 2));
+          const int ex = mx_exponent(amax);
+          const float sc = ldexpf(1.f, -ex);
+          const int64_t row = mbase + r;
+          if (ok) {
+            int lo = 0, hi = 0;
+            lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[0] * sc, a[1] * sc, lo, false);
+            lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[2] * sc, a[3] * sc, lo, true);
+            hi = __builtin_amdgcn_cvt_pk_fp8_f32(a[4] * sc, a[5] * sc, hi, false);
+            hi = __builtin_amdgcn_cvt_pk_fp8_f32(a[6] * sc, a[7] * sc, hi, true);
+            *reinterpret_cast<uint2*>(g.aq + row * g.F + f) = uint2{(unsigned)lo, (unsigned)hi};
+            if (g.C != nullptr) *reinterpret_cast<u32x4*>(g.C + row * g.ldc + f) = av;
+          }
+          if (r < mlen && (q & 3) == 0)
+            g.aqs[((int64_t)nt * g.srows + row) * 4 + (q >> 2)] = (uint8_t)(f < g.F ? ex + 127 : 127);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
@@ -973,7 +1171,7 @@ constexpr int kTileBM = GBM;
 // Wave layout per product: 4 waves of 128x128 (one per SIMD; register-staged refill two slices ahead) for the
 // forward products, whose operands are both k-contiguous; 8 waves of 128x64 (LDS-DMA refill) for the
 // backward products and the fp8 forward.  The row-grouped tile prefix is computed with the kernels' BM.
-constexpr int kNW_fwd1 = 4, kNW_fwd2 = 4, kNW_dact = 8, kNW_dxp = 8, kNW_dwd = 8, kNW_dw1 = 8, kNW_fp8 = 8;
+constexpr int kNW_fwd1 = 4, kNW_fwd2 = 4, kNW_dact = 8, kNW_dxp = 8, kNW_dwd = 8, kNW_dw1 = 8, kNW_fp8 = 4;
 }  // namespace
 }  // namespace moe
 

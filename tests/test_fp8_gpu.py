@@ -143,29 +143,36 @@ def test_layer_forward_fp8():
     assert torch.allclose(layer.quantize_fp8()[1][0], 2.0 * ops.quant_rows_fp8(layer.w_gate.detach() / 2.0)[1])
 
 
-@pytest.mark.parametrize("fp8", [False, True])
-def test_forward_without_preactivations(fp8):
+@pytest.mark.parametrize("fp8,R,H,F", [(False, 600, 256, 512), (True, 600, 256, 512), (True, 700, 4096, 2048)])
+def test_forward_without_preactivations(fp8, R, H, F):
     """keep_preact=False (inference) stores no hgu and leaves act and y bit-identical."""
-    say(f"[swiglu no-preact] fp8={fp8}")
-    R, H, F, E = 600, 256, 512, 4
+    say(f"[swiglu no-preact] fp8={fp8} R={R} H={H} F={F}")
+    E = 4
     g = torch.Generator().manual_seed(11)
     xp = torch.randn(R, H, generator=g).to(torch.bfloat16)
     wts = _weights(E, F, H, 12)
-    offsets = torch.tensor([0, 250, 250, 550, 600], dtype=torch.int32).to(dev())
+    offsets = torch.tensor([0, 250, 250, 550, R], dtype=torch.int32).to(dev())
     if fp8:
         xq, sx = ops.quant_rows_fp8(xp.to(dev()))
         wq = [ops.quant_rows_fp8(w.to(dev())) for w in wts]
-        run = lambda keep: ops.swiglu_forward_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets,
-                                                  keep_preact=keep)
+        def run(keep):
+            a, h, y, (aq, asc) = ops.swiglu_forward_fp8(xq, sx, [q for q, _ in wq], [s for _, s in wq], offsets,
+                                                        keep_preact=keep, return_mx=True)
+            run.mx = (aq.clone(), asc.clone())  # views of the workspace, which the next call reuses
+            return a, h, y
     else:
         xd, wd = xp.to(dev()), [w.to(dev()) for w in wts]
         run = lambda keep: ops.swiglu_forward(xd, *wd, offsets, keep_preact=keep)
     a1, h1, y1 = run(True)
+    mx1 = getattr(run, "mx", None)
     a2, h2, y2 = run(False)
     assert h1 is not None and h2 is None
     assert torch.equal(y1, y2)
     if fp8:
         assert a2 is None  # inference: the down projection reads act block-quantized, no bf16 copy
+        # the inference epilogue (SwiGLU on the accumulators) writes the same e4m3 bytes and E8M0 scales
+        used = int(offsets[-1])
+        assert torch.equal(mx1[0][:used], run.mx[0][:used]) and torch.equal(mx1[1][:used], run.mx[1][:used])
     else:
         assert torch.equal(a1, a2)
 
