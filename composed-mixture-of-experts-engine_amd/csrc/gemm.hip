@@ -952,6 +952,38 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         }
       }
   } else {
+    if constexpr (EPI == 1) {
+      if (g.C2 == nullptr) {
+        // inference (no pre-activations to store): act formed on the accumulators as in the fp8 epilogue above
+        // (gate and up rounded to bf16, act rounded to bf16), and only act goes through LDS, as a [256][128 + 8]
+        // bf16 tile, to leave as 16-byte row chunks
+        constexpr int AP = GBN / 2 + 8;
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int pr = 0; pr < NI / 2; ++pr) {
+            const int cg = wn0 + 2 * pr * 32 + (lane & 31);
+            const int fc = (cg >> 6) * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+              const float gq = __uint_as_float((uint32_t)f2bf(acc[mi][2 * pr][j]) << 16);
+              const float uq = __uint_as_float((uint32_t)f2bf(acc[mi][2 * pr + 1][j]) << 16);
+              cs[r * AP + fc] = f2bf(silu_f(gq) * uq);
+            }
+          }
+        __syncthreads();
+        constexpr int QPR = GBN / 16;  // 8-f chunks per row
+        for (int u = tid; u < GBM * QPR; u += GNT) {
+          const int r = u / QPR, q = u % QPR;
+          const int f = nt * (GBN / 2) + q * 8;
+          if (r >= mlen || f >= g.F) continue;
+          *reinterpret_cast<u32x4*>(g.C + (int64_t)(mbase + r) * g.ldc + f) =
+              *reinterpret_cast<const u32x4*>(&cs[r * AP + q * 8]);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
