@@ -296,57 +296,18 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
   // 128-byte line per row); cols mode -> k-rows 2j + l/32, slot l%32.  Rows / columns past the
   // tile are clamped to valid ones (their results are never stored), so a stage that lies wholly
   // inside the reduction range needs only a wave-uniform step per instruction: rows mode adds k0
-  // elements, cols mode k0 * ld.  Most kernels keep each source as a 64-bit address (a_src, b_src,
-  // b_src2) and the lane's first k within a stage (a_kl, b_kl); the fp8 down projection (rows mode),
-  // whose block scales leave it no registers to spare, keeps a wave-uniform base and the lane's 32-bit
-  // element offset (a_off, b_off) and recomputes the k. ----
+  // elements, cols mode k0 * ld. ----
   const uint16_t* a_src[QPW];
   const uint16_t* b_src[QPW];
   const uint16_t* b_src2[QPW];
-  int a_kl_[QPW], b_kl_[QPW];
-  uint32_t a_off_[QPW], b_off_[QPW];
-  // k slot (l%8) ^ ((i/2)%8) of row i = 8j + l/8, times 8 elements
-  auto kl_rows = [&](int q) { return ((lane & 7) ^ (((8 * (QPW * wv + q) + (lane >> 3)) >> 1) & 7)) * 8; };
-  auto a_kl = [&](int q) {
-    if constexpr (MX) return kl_rows(q);
-    else return a_kl_[q];
-  };
-  auto b_kl = [&](int q) {
-    if constexpr (MX) return kl_rows(q);
-    else return b_kl_[q];
-  };
-  // the bases of the offsets: A rows from mbase, B rows from n0
-  const uint16_t* const a_base = g.A + (int64_t)mbase * g.lda + kbase;
-  const uint16_t* const b_base = g.B + (int64_t)e * g.b_estride + (int64_t)n0 * g.ldb;
-  // In the offsets' uses an empty asm keeps the compiler from hoisting the 64-bit sums out of the k loop
-  // (which would hold two VGPRs per source again).
-  auto a_at = [&](int q, int64_t step) -> const uint16_t* {
-    if constexpr (MX) {
-      uint32_t o = a_off_[q];
-      __asm__("" : "+v"(o));
-      return a_base + step + o;
-    } else {
-      return a_src[q] + step;
-    }
-  };
-  auto b_at = [&](int q, int64_t step) -> const uint16_t* {
-    if constexpr (MX) {
-      uint32_t o = b_off_[q];
-      __asm__("" : "+v"(o));
-      return b_base + step + o;
-    } else {
-      return b_src[q] + step;
-    }
-  };
+  int a_kl_[QPW], b_kl_[QPW];  // the lane's first k within a stage
+  auto a_kl = [&](int q) { return a_kl_[q]; };
+  auto b_kl = [&](int q) { return b_kl_[q]; };
+  auto a_at = [&](int q, int64_t step) -> const uint16_t* { return a_src[q] + step; };
+  auto b_at = [&](int q, int64_t step) -> const uint16_t* { return b_src[q] + step; };
 #pragma unroll
   for (int q = 0; q < QPW; ++q) {
     const int j = QPW * wv + q;
-    if constexpr (MX) {
-      const int ia = min(8 * j + (lane >> 3), mlen - 1), ib = min(8 * j + (lane >> 3), nlen - 1);
-      a_off_[q] = (uint32_t)(ia * g.lda + kl_rows(q));
-      b_off_[q] = (uint32_t)(ib * g.ldb + kl_rows(q));
-      continue;
-    }
     if constexpr (AMODE != 1) {
       const int i = 8 * j + (lane >> 3);
       a_kl_[q] = ((lane & 7) ^ ((i >> 1) & 7)) * 8;
@@ -461,101 +422,8 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         acc[mi][ni] = mfma32x32x16(__builtin_bit_cast(bf16x8, fa[mi]), __builtin_bit_cast(bf16x8, fb[ni]), acc[mi][ni]);
   };
 
-  // Software pipeline over the four 16-wide k quarters of a stage: the LDS reads of quarter q+1 are
-  // interleaved with the MFMAs of quarter q (register sets 0 and 1 alternate).  Before the last
-  // quarter of stage kt every wave waits for stage kt+1 (the only DMA group in flight) and for its
-  // own reads of stage kt; one barrier makes both visible workgroup-wide, and stage kt's two units
-  // are refilled with stage kt+2 while the last quarter's MFMAs run.
-  if constexpr (F8 && NW == 8) {
-    // fp8: two 64-k steps per slice; each step's fragments are read and consumed in turn (the other wave
-    // of the SIMD covers the read latency), one barrier per slice as above.  With block-scaled A (MX) each
-    // slice also brings the A rows' E8M0 scales of its four 32-k blocks: a 2 KB window from the 4-row-aligned
-    // row below the tile's first (srows is a multiple of 4, so it is 16-byte aligned), one 256-byte DMA per
-    // wave, and each lane passes its row's scale of the block it supplies to the MFMA.
-    uint8_t* const mx_lds = smem + GSMEM + GSCALE;
-    const int mx_r0 = mbase & 3;
-    auto issue_mx = [&](int kt) {
-      if constexpr (MX) {
-        const uint8_t* src = g.mxs + ((int64_t)kt * g.srows + (mbase - mx_r0)) * 4 + wv * 256 + lane * 16;
-        if (lane < 16) lds_dma16(src, lds_addr(mx_lds + (kt & 1) * MXSTAGE + wv * 256));
-      }
-    };
-    constexpr int MXI = MX ? 1 : 0;  // DMA instructions per wave per slice for the scales
-    if (nk > 0) {
-      issue_unit(0);
-      issue_unit(1);
-      issue_mx(0);
-      if (nk > 1) {
-        issue_unit(2);
-        issue_unit(3);
-        issue_mx(1);
-      }
-      if (nk > 1) wait_vmcnt<2 * QPW + MXI>();
-      else wait_vmcnt<0>();
-      lds_barrier();
-      for (int kt = 0; kt < nk; ++kt) {
-        const uint8_t* const ca = unit_ptr(2 * kt);
-        const uint8_t* const cb = unit_ptr(2 * kt + 1);
-        if constexpr (MX) {
-          // the slice's four block scales of each of the lane's MI rows (one 4-byte LDS word per row), shifted
-          // so that byte 2 st of the word is block 2 st + h: lane half h supplies the scale of the step's block h
-          int sw[MI];
-#pragma unroll
-          for (int mi = 0; mi < MI; ++mi)
-            sw[mi] = (int)(*reinterpret_cast<const uint32_t*>(
-                         mx_lds + (kt & 1) * MXSTAGE + (mx_r0 + wm0 + mi * 32 + (lane & 31)) * 4) >>
-                     (8 * (lane >> 5)));
-          // the step's B fragments, then A one 32-row block at a time (the next block's read issued before the
-          // current block's MFMAs): two A fragments live instead of MI, which keeps the scales' registers and
-          // the DMA addresses out of scratch
-#pragma unroll
-          for (int st = 0; st < 2; ++st) {
-            i32x8 fb[NI];
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(cb, wn0 + ni * 32, st, lane);
-            i32x8 fa = frag_rows_f8(ca, wm0, st, lane);
-#pragma unroll
-            for (int mi = 0; mi < MI; ++mi) {
-              i32x8 fn;
-              if (mi + 1 < MI) fn = frag_rows_f8(ca, wm0 + (mi + 1) * 32, st, lane);
-#pragma unroll
-              for (int ni = 0; ni < NI; ++ni) {
-                if (st == 0)
-                  acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb[ni], acc[mi][ni], 0, 0, 0,
-                                                                                sw[mi], 0, 127);
-                else
-                  acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb[ni], acc[mi][ni], 0, 0, 2,
-                                                                                sw[mi], 0, 127);
-              }
-              __builtin_amdgcn_sched_barrier(0);
-              if (mi + 1 < MI) fa = fn;
-            }
-          }
-        } else {
-#pragma unroll
-          for (int st = 0; st < 2; ++st) {
-            i32x8 fa[MI], fb[NI];
-#pragma unroll
-            for (int mi = 0; mi < MI; ++mi) fa[mi] = frag_rows_f8(ca, wm0 + mi * 32, st, lane);
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) fb[ni] = frag_rows_f8(cb, wn0 + ni * 32, st, lane);
-#pragma unroll
-            for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-              for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32x32x64_f8(fa[mi], fb[ni], acc[mi][ni]);
-          }
-        }
-        wait_vmcnt_lgkm0<0>();  // stage kt+1 landed; this wave's reads of stage kt are done
-        lds_barrier();
-        if (kt + 2 < nk) {
-          issue_unit(2 * kt + 4);
-          issue_unit(2 * kt + 5);
-          issue_mx(kt + 2);
-        }
-      }
-      wait_vmcnt<0>();
-    }
-  } else if constexpr (NW == 4) {
+  static_assert(!F8 || NW == 4, "the fp8 products run the 4-wave loop");
+  if constexpr (NW == 4) {
     static_assert(AMODE == BMODE && AMODE != 1, "the 4-wave main loop takes k-contiguous operands");
     // One wave per SIMD, 128x128 per wave.  The refill goes through registers two slices ahead: while slice
     // kt is computed, each wave writes its share of slice kt+1 (loaded during slice kt-1) into the free LDS
@@ -817,6 +685,11 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
     }
     wait_vmcnt<0>();
   } else if (nk > 0) {
+    // Software pipeline over the four 16-wide k quarters of a stage: the LDS reads of quarter q+1 are
+    // interleaved with the MFMAs of quarter q (register sets 0 and 1 alternate).  Before the last
+    // quarter of stage kt every wave waits for stage kt+1 (the only DMA group in flight) and for its
+    // own reads of stage kt; one barrier makes both visible workgroup-wide, and stage kt's two units
+    // are refilled with stage kt+2 while the last quarter's MFMAs run.
     issue_unit(0);
     issue_unit(1);
     if (nk > 1) {
