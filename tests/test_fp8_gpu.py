@@ -82,6 +82,8 @@ def _weights(E, F, H, seed):
     (600, 256, 512, 4, [250, 0, 300, 50]),        # an empty expert, ragged segments, rows past offsets[E]
     (512, 4096, 14336, 2, [300, 212]),            # the C4 expert shape
     (96, 128, 64, 3, [1, 90, 5]),                 # segments shorter than a tile, F < a 256-column tile
+    (200, 384, 416, 2, [120, 80]),                # 3 k slices in the gate/up product; 4 in the down
+                                                  # projection, the last partial (32 of 128)
 ])
 def test_swiglu_forward_fp8_parity(R, H, F, E, counts):
     say(f"[fp8 swiglu] R={R} H={H} F={F} E={E}")
