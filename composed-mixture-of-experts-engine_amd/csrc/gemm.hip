@@ -6,8 +6,8 @@
 // (128 KB) of 64-wide k slices, in one of two forms:
 //   8 waves of 128x64, the ring filled by LDS-DMA (global_load_lds_dwordx4) so
 //     no operand passes through VGPRs (the backward products, whose operands
-//     are read with transposing LDS reads, and the fp8 forward);
-//   4 waves of 128x128, one per SIMD (the two bf16 forward products): a third
+//     are read with transposing LDS reads);
+//   4 waves of 128x128, one per SIMD (the forward products, bf16 and fp8): a third
 //     fewer LDS fragment bytes per MFMA; the refill goes through registers two
 //     slices ahead, one 16-byte piece at a time between the MFMAs, with every
 //     MFMA slot of a k quarter carrying at most one fragment read and one
@@ -43,9 +43,11 @@
 //          (sa) and per B row (sb, sb2 for the up rows of EPI1).  The host passes K and the leading
 //          dimensions in 16-bit units (two fp8 per unit), so the DMA and the LDS tile are byte-for-byte
 //          those of a bf16 rows tile: a 64-unit slice holds 128 fp8 k.  Each k step of 64 uses
-//          v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales) on 32-byte fragments made of two 16-byte
-//          reads (A and B use the same k-to-lane map, which is all the product needs), and the
-//          epilogue multiplies by sa[row] * sb[col] before rounding.
+//          v_mfma_scale_f32_32x32x64_f8f6f4 on 32-byte fragments made of two 16-byte reads (A and B
+//          use the same k-to-lane map, which is all the product needs), and the epilogue multiplies by
+//          sa[row] * sb[col] before rounding.  The gate/up product (EPI1) writes act block-quantized
+//          (e4m3 plus an E8M0 scale per 32 values, aq / aqs), and the down projection passes those
+//          block scales to the MFMA (mxs; its sa is then 1).
 //
 // products (R = rows, per expert e):
 //   fwd1  [act | hgu] = xp  . [Wg_e ; Wu_e]^T      A rows(xp), B rows(W),  G0, EPI1
@@ -486,7 +488,7 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
       // (global loads) go one per MFMA slot into step 0 and the first half of step 1; then each wave waits
       // for its own LDS traffic, one barrier makes slice kt+1 visible, and the second half of step 1 reads
       // slice kt+1's step-0 fragments as they free up.  With block-scaled A (MX) the slice's scale window (2 KB
-      // from the 4-row-aligned row below the tile's first, as the 8-wave loop stages it) rides along as one
+      // from the 4-row-aligned row below the tile's first row) rides along as one
       // more piece (512 bytes a wave, lanes 32-63 repeating lanes 0-31) into a 2-slot LDS area, and each lane reads its rows' scale
       // words of slice kt+1 right after that barrier.
       constexpr int NPX = NP + (MX ? 1 : 0);  // pieces per slice, the scale window last
@@ -1074,8 +1076,8 @@ int launch(const char* name, hipStream_t s, const GemmArgs& a, int64_t R) {
 
 constexpr int kTileBM = GBM;
 // Wave layout per product: 4 waves of 128x128 (one per SIMD; register-staged refill two slices ahead) for the
-// forward products, whose operands are both k-contiguous; 8 waves of 128x64 (LDS-DMA refill) for the
-// backward products and the fp8 forward.  The row-grouped tile prefix is computed with the kernels' BM.
+// forward products (bf16 and fp8), whose operands are both k-contiguous; 8 waves of 128x64 (LDS-DMA refill)
+// for the backward products.  The row-grouped tile prefix is computed with the kernels' BM.
 constexpr int kNW_fwd1 = 4, kNW_fwd2 = 4, kNW_dact = 8, kNW_dxp = 8, kNW_dwd = 8, kNW_dw1 = 8, kNW_fp8 = 4;
 }  // namespace
 }  // namespace moe
