@@ -762,21 +762,25 @@ __global__ __launch_bounds__(NW * 64, 1) void k_gemm(GemmArgs g) {
         // through LDS, as a [256][128 + 8] bf16 tile, for the block quantization (the same per-chunk code as
         // the general path, reading one 16-byte act chunk instead of the gate and up chunks)
         constexpr int AP = GBN / 2 + 8;
+        static_assert(NI == 4, "two gate/up pairs per wave");
+        // column scales of the lane's two pairs (gate, up); each row scale is read once for both pairs, and
+        // each bf16 rounding converts two values at once (the same rounding as one at a time)
+        const int cg0 = wn0 + (lane & 31), cg1 = cg0 + 64;
+        const float sg0 = s_sc[256 + cg0], su0 = s_sc[256 + cg0 + 32];
+        const float sg1 = s_sc[256 + cg1], su1 = s_sc[256 + cg1 + 32];
+        const int fc0 = (cg0 >> 6) * 32 + (lane & 31), fc1 = (cg1 >> 6) * 32 + (lane & 31);
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-          for (int pr = 0; pr < NI / 2; ++pr) {
-            const int cg = wn0 + 2 * pr * 32 + (lane & 31);
-            const float sg = s_sc[256 + cg], su = s_sc[256 + cg + 32];
-            const int fc = (cg >> 6) * 32 + (lane & 31);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
-              const float sr = s_sc[r];
-              const float gq = __uint_as_float((uint32_t)f2bf(acc[mi][2 * pr][j] * sr * sg) << 16);
-              const float uq = __uint_as_float((uint32_t)f2bf(acc[mi][2 * pr + 1][j] * sr * su) << 16);
-              cs[r * AP + fc] = f2bf(silu_f(gq) * uq);
-            }
+          for (int j = 0; j < 16; ++j) {
+            const int r = wm0 + mi * 32 + (j >> 2) * 8 + (lane >> 5) * 4 + (j & 3);
+            const float sr = s_sc[r];
+            const uint32_t gu0 = pack2bf(acc[mi][0][j] * sr * sg0, acc[mi][1][j] * sr * su0);
+            const uint32_t gu1 = pack2bf(acc[mi][2][j] * sr * sg1, acc[mi][3][j] * sr * su1);
+            const uint32_t a01 = pack2bf(silu_f(__uint_as_float(gu0 << 16)) * __uint_as_float(gu0 & 0xffff0000u),
+                                         silu_f(__uint_as_float(gu1 << 16)) * __uint_as_float(gu1 & 0xffff0000u));
+            cs[r * AP + fc0] = (uint16_t)a01;
+            cs[r * AP + fc1] = (uint16_t)(a01 >> 16);
           }
         __syncthreads();
         constexpr int QPR = GBN / 16;  // 8-f chunks per row
