@@ -509,7 +509,8 @@ def swiglu_forward_fp8(xq, sx, wq, wscale, offsets, out_dtype=torch.bfloat16, ke
     (gate [E,F,H], up [E,F,H], down [E,H,F]) e4m3 bytes with ``wscale`` = (sg [E,F], su [E,F], sd [E,H])
     -> (act [R,F], hgu [R,2F], y [R,H]) bf16, as :func:`swiglu_forward`; with keep_preact=False (inference)
     act and hgu are None (the down projection reads act block-quantized from the gate/up epilogue).
-    ``return_mx``: also return (act e4m3 bytes [R, F], E8M0 block scales [R, F/32]) as the kernels wrote them."""
+    ``return_mx``: also return (act e4m3 bytes [R, F], E8M0 block scales [R, F/32]) as the kernels wrote them:
+    views of the call's workspace, valid until the next call that takes the same workspace (clone to keep them)."""
     wg, wu, wd = wq
     sg, su, sd = wscale
     dev = L.require_device(xq, sx, wg, wu, wd, sg, su, sd, offsets)
