@@ -1,6 +1,6 @@
 """The MoE layer at the benchmark's own full sizes: C4 (T=8192, d=4096, E=8, F=14336, K=2, reference layout:
 the headline workload) and C5 (T=32768, d=2048, E=128, F=768, K=8, routed layout, Zipf(1.1) logit bias,
-capacity factor 1.0 with drops, aux and z losses).
+capacity factor 1.0 with drops, aux and z losses); and C4's fp8 inference forward.
 
 Inputs have the configs' shapes and scales, drawn on the device from fixed seeds (the CPU draw the benchmark
 uses takes minutes for C4's 2.8 GB of weights).  Checks:
@@ -172,3 +172,42 @@ def test_c5_skewed_routed_full_size():
     cnt = np.diff(pl["offsets"])
     assert cnt.max() > 8 * max(1, int(np.median(cnt)))
     assert layer.router.last_profile.expert_load_imbalance > 4.0
+
+
+def test_c4_fp8_forward_full_size():
+    """The C4 layer's fp8 inference forward at full size: within the e4m3 rounding of the bf16 forward, and the
+    last expert's last rows (the grid's last tiles) through the float64 oracle chain from the kernels' own
+    quantized operands, with the block-quantized act bit-exact."""
+    from moe_mi355 import ops
+    from oracle import fp8 as O8
+
+    cfg = configs.C4
+    say(f"[fullsize] {cfg.name} fp8 forward")
+    inp = _inputs(cfg, seed=3)
+    layer = DistributedMoELayer(cfg.H, cfg.F, cfg.E, cfg.K, build_topology(), dtype=cfg.dtype,
+                                layout="reference").to(dev())
+    with torch.no_grad():
+        for name in ("w_gate", "w_up", "w_down"):
+            getattr(layer, name).copy_(inp[name])
+        layer.router.gate_w.copy_(inp["gate_w"])
+        ref = layer(inp["x"])
+    out = layer.forward_fp8(inp["x"])
+    torch.cuda.synchronize()
+    err = ((out.float() - ref.float()).abs().max() / ref.float().abs().max()).item()
+    assert err < 0.1, err
+    p = layer.last_plan
+    wq, ws = layer.quantize_fp8()
+    xq, sx = ops.permute_fp8(inp["x"], p)
+    act, _hgu, y, (aq, asc) = ops.swiglu_forward_fp8(xq, sx, wq, ws, p.offsets, return_mx=True)
+    torch.cuda.synchronize()
+    offs = p.offsets.cpu().tolist()
+    e = cfg.E - 1
+    hi = int(offs[e + 1])
+    lo = hi - 48
+    assert lo >= int(offs[e])
+    mq, ms = O8.quant_mx(act[lo:hi].cpu().float())
+    assert torch.equal(aq[lo:hi].cpu(), mq) and torch.equal(asc[lo:hi].cpu(), ms)
+    one = lambda t: t[e:e + 1].cpu()  # noqa: E731
+    _rh, _ra, ry = O8.swiglu_fwd_fp8(xq[lo:hi].cpu(), sx[lo:hi].cpu(), [one(w) for w in wq], [one(s) for s in ws],
+                                     [0, hi - lo], act_in=act[lo:hi].cpu().float())
+    assert_rel(y[lo:hi], ry, 2e-2, "y (last rows)")
